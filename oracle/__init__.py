@@ -1,0 +1,138 @@
+"""CPU oracle for Juno's quantized matvec path -- TEST INFRASTRUCTURE ONLY.
+
+This package is the checker for the HIP library.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it; the product package ``juno_amd`` never does.
+
+It wraps ``oracle/_build/libjuno_oracle.so``, a C restatement of the Java CPU
+path (citations per function in ``juno_oracle.c``):
+
+* ``f16_to_f32``      GgufReader.f16ToF32        (GgufReader.java:1248-1271)
+* ``f32_to_f16``      LoraMerge.f32ToF16          (LoraMerge.java:589-605)
+* ``java_round``      java.lang.Math.round(float)
+* ``dequantize``      LlamaTransformerHandler.dequantize* (LlamaTransformerHandler.java:873-1135)
+* ``matvec``          LlamaTransformerHandler.matVec(QuantizedTensor, ...)
+                      (LlamaTransformerHandler.java:1200-1254, 1428-1638)
+* ``quantize``        LoraMerge.requantize        (LoraMerge.java:226-469)
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "libjuno_oracle.so")
+
+F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
+QK = {F32: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {F32: 4, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+
+_lib = None
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        L.or_f16_to_f32.restype = ctypes.c_float
+        L.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.or_f16_to_f32_bits.restype = ctypes.c_uint32
+        L.or_f16_to_f32_bits.argtypes = [ctypes.c_uint16]
+        L.or_f32_to_f16.restype = ctypes.c_uint16
+        L.or_f32_to_f16.argtypes = [ctypes.c_float]
+        L.or_java_round.restype = ctypes.c_int32
+        L.or_java_round.argtypes = [ctypes.c_float]
+        L.or_raw_byte_count.restype = ctypes.c_int64
+        L.or_raw_byte_count.argtypes = [ctypes.c_int, ctypes.c_int64]
+        L.or_q4k_scale.argtypes = [P, ctypes.c_int]
+        L.or_q4k_min.argtypes = [P, ctypes.c_int]
+        L.or_dequantize.argtypes = [ctypes.c_int, P, ctypes.c_int, ctypes.c_int, P]
+        L.or_matvec.argtypes = [ctypes.c_int, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                P, ctypes.c_int]
+        L.or_quantize.argtypes = [ctypes.c_int, P, ctypes.c_int64, P]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def f16_to_f32(bits: int) -> float:
+    return lib().or_f16_to_f32(bits & 0xFFFF)
+
+
+def f32_to_f16(v: float) -> int:
+    return lib().or_f32_to_f16(v)
+
+
+def java_round(v: float) -> int:
+    return lib().or_java_round(v)
+
+
+def raw_byte_count(qtype: int, nelems: int) -> int:
+    return lib().or_raw_byte_count(qtype, nelems)
+
+
+def q4k_scale(sc: bytes, j: int) -> int:
+    b = np.frombuffer(bytes(sc), dtype=np.uint8).copy()
+    return lib().or_q4k_scale(_ptr(b), j)
+
+
+def q4k_min(sc: bytes, j: int) -> int:
+    b = np.frombuffer(bytes(sc), dtype=np.uint8).copy()
+    return lib().or_q4k_min(_ptr(b), j)
+
+
+def _as_u8(raw) -> np.ndarray:
+    if isinstance(raw, (bytes, bytearray, memoryview)):
+        return np.frombuffer(bytes(raw), dtype=np.uint8)
+    return np.ascontiguousarray(raw, dtype=np.uint8)
+
+
+def dequantize(qtype: int, raw, rows: int, cols: int) -> np.ndarray:
+    raw = _as_u8(raw)
+    if raw.size != raw_byte_count(qtype, rows * cols):
+        raise ValueError("raw size does not match rows*cols")
+    out = np.empty(rows * cols, dtype=np.float32)
+    if lib().or_dequantize(qtype, _ptr(raw), rows, cols, _ptr(out)) != 0:
+        raise ValueError(f"dequantize: unsupported type {qtype} or cols {cols}")
+    return out.reshape(rows, cols)
+
+
+def matvec(qtype: int, raw, x: np.ndarray, row_start: int, row_end: int, cols: int,
+           nthreads: int = 0) -> np.ndarray:
+    raw = _as_u8(raw)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.size != cols:
+        raise ValueError("x.length != cols")
+    pitch = cols // QK[qtype] * BLOCK_BYTES[qtype]
+    if row_end * pitch > raw.size:
+        raise ValueError("row range exceeds the tensor")
+    y = np.empty(row_end - row_start, dtype=np.float32)
+    if lib().or_matvec(qtype, _ptr(raw), _ptr(x), row_start, row_end, cols, _ptr(y), nthreads) != 0:
+        raise ValueError(f"matvec: unsupported type {qtype} or cols {cols}")
+    return y
+
+
+def quantize(qtype: int, data: np.ndarray) -> np.ndarray:
+    data = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
+    n = data.size
+    if n % QK[qtype]:
+        raise ValueError("n is not a block multiple")
+    out = np.zeros(raw_byte_count(qtype, n), dtype=np.uint8)
+    if lib().or_quantize(qtype, _ptr(data), n, _ptr(out)) != 0:
+        raise ValueError(f"quantize: unsupported type {qtype}")
+    return out
