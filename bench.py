@@ -1,0 +1,299 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized GEMV hot path on one MI355X.
+
+Workload: the GEMVs of one Llama-3-8B-shaped
+Q4_K_M decode step at B=1 -- 32 layers x {q 4096x4096, k 1024x4096, v 1024x4096,
+o 4096x4096, gate 14336x4096, up 14336x4096, down 4096x14336} plus the
+lm_head 128256x4096.  Q4_K_M type rule used here: attn_v, ffn_down and the
+lm_head are Q6_K in every layer, everything else Q4_K (4.876 GB of packed
+weights per token).  Weights are random N(0, 0.02) fp32 drawn on the device and
+quantized on the device with LoraMerge's Q4_K / Q6_K quantizers; activations are
+N(0, 1) fp32.  All inputs are resident in HBM before timing starts.
+
+A "step" is one decode token's 225 GEMVs, captured once into a HIP graph and
+replayed.  value = algorithmic bytes per step / step time (GB/s), where
+algorithmic bytes = packed weight bytes + 4*(cols + rows) per GEMV.
+
+Extra measurements in the same JSON line:
+  roofline      the dominant kernel (Q4_K gate/up GEMV 14336x4096), timed with
+                HIP events on its own stream over all 64 gate/up matrices
+  cpu_baseline  the CPU oracle (C restatement of Juno's Java matVecQ4Kraw /
+                matVecQ6Kraw, one task per row on a thread pool) on one layer's
+                GEMVs, on the host cores of this machine
+  batched       the same step with B = 32 activations per GEMV
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+Q4_K, Q6_K = 12, 14
+BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210)}
+
+HIDDEN, FFN, KV, VOCAB, LAYERS = 4096, 14336, 1024, 128256, 32
+# (name, rows, cols, type)
+LAYER = [("attn_q", HIDDEN, HIDDEN, Q4_K), ("attn_k", KV, HIDDEN, Q4_K), ("attn_v", KV, HIDDEN, Q6_K),
+         ("attn_output", HIDDEN, HIDDEN, Q4_K), ("ffn_gate", FFN, HIDDEN, Q4_K), ("ffn_up", FFN, HIDDEN, Q4_K),
+         ("ffn_down", HIDDEN, FFN, Q6_K)]
+HEAD = ("output", VOCAB, HIDDEN, Q6_K)
+
+
+def packed_bytes(rows, cols, t):
+    qk, bb = BLOCK[t]
+    return rows * (cols // qk) * bb
+
+
+def algo_bytes(rows, cols, t, B=1):
+    return packed_bytes(rows, cols, t) + 4 * B * (rows + cols)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_model(torch, be, seed=0):
+    """Device-resident packed weights for all layers + head."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    mats = []
+    for layer in range(LAYERS):
+        for name, rows, cols, t in LAYER:
+            w = torch.randn(rows * cols, generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
+            mats.append((f"blk.{layer}.{name}", rows, cols, t,
+                         be.quantize_dev(t, w.data_ptr(), rows, cols, torch.cuda.current_stream().cuda_stream)))
+            del w
+    name, rows, cols, t = HEAD
+    w = torch.randn(rows * cols, generator=g, device="cuda", dtype=torch.float32).mul_(0.02)
+    mats.append((name, rows, cols, t, be.quantize_dev(t, w.data_ptr(), rows, cols,
+                                                       torch.cuda.current_stream().cuda_stream)))
+    del w
+    torch.cuda.synchronize()
+    return mats
+
+
+def make_step(torch, L, mats, B, stream):
+    """Buffers and a launcher for one decode step's GEMVs at batch B."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1)
+    xs = {HIDDEN: torch.randn(B, HIDDEN, generator=g, device="cuda"),
+          FFN: torch.randn(B, FFN, generator=g, device="cuda")}
+    ys = {r: torch.empty(B, r, device="cuda") for r in {m[1] for m in mats}}
+
+    def launch():
+        s = ctypes.c_void_p(stream.cuda_stream)
+        for _, rows, cols, _, dev in mats:
+            rc = L.jh_qmatvec_batched_dev(dev.handle, xs[cols].data_ptr(), B, ys[rows].data_ptr(), 0, rows, s)
+            if rc:
+                raise RuntimeError(L.jh_last_error().decode())
+    return launch, xs, ys
+
+
+def time_graph(torch, launch, stream, steps, warmup):
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        launch()  # eager run once (also validates arguments)
+        stream.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            launch()
+        for _ in range(warmup):
+            g.replay()
+        stream.synchronize()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            g.replay()
+        e1.record(stream)
+        stream.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / steps, wall / steps * 1e3
+
+
+def dominant_kernel(torch, L, mats, stream, reps):
+    """Average launch duration of the Q4_K gate/up GEMV (14336x4096, B=1),
+    HIP events on the launch stream, rotating over the 64 distinct matrices."""
+    sel = [m for m in mats if m[0].endswith(("ffn_gate", "ffn_up"))]
+    x = torch.randn(HIDDEN, device="cuda")
+    y = torch.empty(FFN, device="cuda")
+    s = ctypes.c_void_p(stream.cuda_stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # one graph of the 64 launches, replayed: no host launch gaps inside the timed region
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            for _, rows, _, _, dev in sel:
+                L.jh_qmatvec_batched_dev(dev.handle, x.data_ptr(), 1, y.data_ptr(), 0, rows, s)
+        g.replay()
+        stream.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        stream.synchronize()
+    avg_ms = e0.elapsed_time(e1) / (reps * len(sel))
+    per_launch = algo_bytes(FFN, HIDDEN, Q4_K)
+    return avg_ms, per_launch, sel
+
+
+def d2h_packed(torch, dev):
+    """Copy a matrix's packed bytes to host memory."""
+    import numpy as np
+    hbuf = np.empty(dev.nbytes(), dtype=np.uint8)
+    torch.cuda.synchronize()
+    rc = torch.cuda.cudart().cudaMemcpy(hbuf.ctypes.data, dev.device_pointer(), dev.nbytes(), 2)
+    if int(rc) != 0:
+        raise RuntimeError(f"D2H copy failed: {rc}")
+    return hbuf
+
+
+def cpu_baseline(torch, mats, budget_s):
+    """CPU oracle (C restatement of the Java path) on layer 0's seven GEMVs."""
+    import numpy as np
+
+    import oracle
+    threads = min(os.cpu_count() or 1, 16)
+    layer0 = [m for m in mats if m[0].startswith("blk.0.")]
+    host = []
+    for name, rows, cols, t, dev in layer0:
+        hbuf = d2h_packed(torch, dev)
+        host.append((name, rows, cols, t, hbuf, np.random.default_rng(3).standard_normal(cols).astype(np.float32)))
+    layer_bytes = sum(algo_bytes(r, c, t) for _, r, c, t, _, _ in host)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for _, rows, cols, t, raw, x in host:
+            oracle.matvec(t, raw, x, 0, rows, cols, nthreads=threads)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    gbs = layer_bytes * reps / dt / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"C restatement of Juno's Java matVecQ4Kraw/matVecQ6Kraw (oracle/juno_oracle.c, "
+                      f"-O2 -ffp-contract=off, one task per row) on layer 0's 7 GEMVs "
+                      f"({layer_bytes / 1e6:.1f} MB), {reps} reps in {dt:.1f} s",
+            "tok_s_equiv": round(gbs * 1e9 / step_bytes(1), 4)}
+
+
+def step_bytes(B):
+    tot = sum(algo_bytes(r, c, t, B) for _, r, c, t in LAYER) * LAYERS
+    return tot + algo_bytes(HEAD[1], HEAD[2], HEAD[3], B)
+
+
+def parity_spot_check(torch, L, mats, stream):
+    """Gate GEMV of layer 0 against the oracle (rel-err metric of the tests)."""
+    import numpy as np
+
+    import oracle
+    name, rows, cols, t, dev = [m for m in mats if m[0] == "blk.0.ffn_gate"][0]
+    hraw = d2h_packed(torch, dev)
+    x = np.random.default_rng(9).standard_normal(cols).astype(np.float32)
+    dx = torch.from_numpy(x).cuda()
+    dy = torch.empty(rows, device="cuda")
+    L.jh_qmatvec_batched_dev(dev.handle, dx.data_ptr(), 1, dy.data_ptr(), 0, rows, None)
+    torch.cuda.synchronize()
+    y = dy.cpu().numpy().astype(np.float64)
+    ref = oracle.matvec(t, hraw, x, 0, rows, cols).astype(np.float64)
+    deq = oracle.dequantize(t, hraw, rows, cols).astype(np.float64)
+    scale = np.abs(deq) @ np.abs(x.astype(np.float64))
+    return float((np.abs(y - ref) / np.maximum(np.abs(ref), 1e-3 * scale)).max())
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline work")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-batched", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the GEMV shards by rows; see the sharding note in DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from juno_amd import _lib
+    from juno_amd import matvec as mv
+    L = _lib.load()
+    ctx = mv.GpuContext.shared(0)
+    be = ctx.create_mat_vec()
+    info = mv.device_info(0)
+    log(f"device {info}")
+    t0 = time.perf_counter()
+    mats = build_model(torch, be)
+    log(f"model built: {len(mats)} matrices, {sum(m[4].nbytes() for m in mats) / 1e9:.3f} GB packed, "
+        f"{time.perf_counter() - t0:.1f} s")
+    stream = torch.cuda.Stream()
+
+    launch, _, _ = make_step(torch, L, mats, 1, stream)
+    ms, wall_ms = time_graph(torch, launch, stream, args.steps, args.warmup)
+    sb = step_bytes(1)
+    gbs = sb / (ms * 1e-3) / 1e9
+    log(f"B=1 step: {ms:.4f} ms (wall {wall_ms:.4f} ms)  {gbs:.1f} GB/s  {1e3 / ms:.1f} tok/s")
+
+    avg_ms, per_launch, _ = dominant_kernel(torch, L, mats, stream, reps=max(args.steps // 5, 4))
+    ach = per_launch / (avg_ms * 1e-3) / 1e9
+    log(f"gate/up Q4_K GEMV: {avg_ms * 1e3:.2f} us/launch  {ach:.1f} GB/s")
+
+    batched = None
+    if not args.no_batched:
+        launch32, _, _ = make_step(torch, L, mats, 32, stream)
+        ms32, _ = time_graph(torch, launch32, stream, max(args.steps // 5, 3), 2)
+        sb32 = step_bytes(32)
+        batched = {"B": 32, "ms_per_step": round(ms32, 4), "tok_s": round(32 * 1e3 / ms32, 1),
+                   "GB_s": round(sb32 / (ms32 * 1e-3) / 1e9, 1)}
+        log(f"B=32 step: {ms32:.4f} ms  {batched}")
+
+    parity = parity_spot_check(torch, L, mats, stream)
+    log(f"parity spot check (layer-0 gate vs oracle): max rel-err {parity:.2e}")
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(torch, mats, args.cpu_budget)
+    if cpu:
+        log(f"cpu baseline: {cpu}")
+
+    line = {
+        "metric": "Q4_K GEMV effective HBM GB/s (% of peak); decode tok/s at 8B shapes, B=1/32",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: N(0,0.02) weights quantized on device with LoraMerge Q4_K/Q6_K; N(0,1) activations",
+        "config": {"workload": "llama3-8b-q4_k_m-decode-gemvs-b1", "hidden": HIDDEN, "ffn": FFN,
+                   "kv_dim": KV, "vocab": VOCAB, "layers": LAYERS, "batch": 1,
+                   "gemvs_per_step": len(mats), "q6k_rule": "attn_v, ffn_down, output in every layer",
+                   "algorithmic_bytes_per_step": sb},
+        "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+        "tok_s": round(1e3 / ms, 1),
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "gemv_q4k 14336x4096 B=1", "avg_launch_us": round(avg_ms * 1e3, 3),
+                     "algorithmic_bytes_per_launch": per_launch},
+        "cpu_baseline": cpu,
+        "batched": batched,
+        "parity_max_rel_err": parity,
+        "device": info["name"],
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

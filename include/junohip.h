@@ -1,0 +1,143 @@
+/*
+ * junohip.h -- C ABI of libjunohip.so, the MI355X (gfx950) quantized matvec
+ * library that replaces the GPU side of Juno's matvec boundary.
+ *
+ * Reference interfaces replaced (paths under /root/reference/node/src/main/java/cab/ml/juno/node/):
+ *   MatVec.sgemv(...)                        MatVec.java:56-90
+ *   GpuMatVec.upload/uploadHalf/...          GpuMatVec.java:38-70
+ *   RocmMatVec (rocBLAS sgemv / hssgemv)     RocmMatVec.java:52-452
+ *   RocmBindings / GpuContext / Device*Matrix RocmBindings.java:61-287, GpuContext.java:58-268,
+ *                                            DeviceFloatMatrix.java:39-111, DeviceHalfMatrix.java:41-115
+ *   RocmAvailability                         RocmAvailability.java:32-128
+ *   static matVec(QuantizedTensor, x, rowStart, rowEnd, cols)
+ *                                            LlamaTransformerHandler.java:1200-1254
+ *   LlamaTransformerHandler.dequantize       LlamaTransformerHandler.java:873-885
+ *   LoraMerge.requantize                     LoraMerge.java:226-241
+ *
+ * Conventions
+ *   - Every function returns an int status: JH_OK (0) or a JH_E* code.  The
+ *     message of the last failure on the calling thread is jh_last_error().
+ *   - Messages follow the reference: dimension errors name "rows*cols" or
+ *     "cols" (MatVecBackendContractTest.java:196-212); HIP failures read
+ *     "<op> failed: rc=N" (GpuBindings.java:180-183); out-of-memory errors
+ *     contain "hipMalloc" so the handlers' CPU fallback keeps working
+ *     (LlamaTransformerHandler.java:340-357).
+ *   - Weight matrices are W[rows][cols] row-major in GGUF packed blocks along
+ *     cols, exactly the bytes of GgufReader.QuantizedTensor.data()
+ *     (GgufReader.java:319-339).  Supported ggml types: 0 (F32), 8 (Q8_0),
+ *     12 (Q4_K), 14 (Q6_K).
+ *   - Host-pointer entry points are synchronous and thread-safe: each host
+ *     thread has its own HIP stream and staging buffers per device.
+ *   - Device-pointer entry points (*_dev) enqueue on the given stream
+ *     (NULL = the default stream) and return without synchronising.
+ */
+#ifndef JUNOHIP_H
+#define JUNOHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    JH_OK = 0,
+    JH_EINVAL = 1,       /* IllegalArgumentException in the reference */
+    JH_ENOMEM = 2,       /* device allocation failed ("hipMalloc failed ...") */
+    JH_EHIP = 3,         /* IllegalStateException("<op> failed: rc=N") */
+    JH_EUNSUPPORTED = 4, /* UnsupportedOperationException (ggml type) */
+    JH_ECLOSED = 5,      /* IllegalStateException("... is closed") */
+    JH_ENODEV = 6,       /* no usable gfx950 device */
+};
+
+enum {
+    JH_TYPE_F32 = 0,
+    JH_TYPE_Q8_0 = 8,
+    JH_TYPE_Q4_K = 12,
+    JH_TYPE_Q6_K = 14,
+};
+
+typedef struct jh_ctx jh_ctx;
+typedef struct jh_qmat jh_qmat;
+
+/* Thread-local message of the last failing call on this thread ("" if none).
+ * Replaces GpuBindings.check's exception text (GpuBindings.java:180-183). */
+const char *jh_last_error(void);
+
+/* Library version string, e.g. "junohip 0.1 gfx950". */
+const char *jh_version(void);
+
+/* Device discovery; replaces RocmAvailability.isAvailable / device queries
+ * (RocmAvailability.java:32-128, RocmBindings.java:208-238). */
+int jh_device_count(int *count);
+int jh_device_info(int device, char name[256], uint64_t *vram_bytes, char arch[64]);
+
+/* Process-wide shared context per device, reference counted; replaces
+ * GpuContext.shared(dev) (GpuContext.java:109-120). */
+int jh_ctx_create(int device, jh_ctx **out);
+int jh_ctx_destroy(jh_ctx *ctx);
+
+/* GgufReader.rawByteCount (GgufReader.java:347-360) for the supported types. */
+int jh_raw_byte_count(int ggml_type, int64_t nelems, int64_t *out);
+
+/* Copy packed bytes host->device unchanged and keep them resident; replaces
+ * GpuMatVec.upload / uploadHalf (GpuMatVec.java:38-58) and the dequantize->fp16
+ * upload of LlamaTransformerHandler.java:296-358.  nbytes must equal
+ * rawByteCount(type, rows*cols) and cols must be a multiple of the block size. */
+int jh_qmat_upload(jh_ctx *ctx, int ggml_type, const void *raw, size_t nbytes, int rows, int cols,
+                   jh_qmat **out);
+
+/* Quantize a device fp32 matrix [rows][cols] into a new resident packed matrix
+ * with LoraMerge's quantizers (LoraMerge.java:226-469), on the device. */
+int jh_qmat_quantize_dev(jh_ctx *ctx, int ggml_type, const float *d_src, int rows, int cols,
+                         void *stream, jh_qmat **out);
+
+/* Release the device memory and the handle (DeviceHalfMatrix.close(),
+ * DeviceHalfMatrix.java:107-114).  NULL is accepted; the handle is invalid
+ * afterwards, so idempotent close() lives in the binding, which clears its
+ * pointer. */
+int jh_qmat_free(jh_qmat *m);
+
+/* Shape, type, size and device address of the packed bytes. */
+int jh_qmat_info(const jh_qmat *m, int *ggml_type, int *rows, int *cols, size_t *nbytes,
+                 const void **d_raw);
+
+/* y[r - row_start] = sum_c deq(W[r][c]) * x[c] for r in [row_start, row_end).
+ * Host x[cols] in, host y[row_end-row_start] out, synchronous; x is not
+ * mutated.  Replaces sgemv(DeviceHalfMatrix, x) (RocmMatVec.java:272-329) and
+ * matVec(QuantizedTensor, x, rowStart, rowEnd, cols)
+ * (LlamaTransformerHandler.java:1200-1212). */
+int jh_qmatvec(jh_ctx *ctx, const jh_qmat *m, const float *x, float *y, int row_start, int row_end);
+
+/* B right-hand sides at once: X[B][cols] in, Y[B][row_end-row_start] out,
+ * row-major, host pointers, synchronous.  Equal, to the GEMV tolerance, to B
+ * independent jh_qmatvec calls.  This is the batched entry point the
+ * reference's InferencePipeline.forwardBatch lacks (InferencePipeline.java:62-69). */
+int jh_qmatvec_batched(jh_ctx *ctx, const jh_qmat *m, const float *X, int B, float *Y, int row_start,
+                       int row_end);
+
+/* Full fp32 dequantization W[rows][cols] to host memory, bit-exact with
+ * LlamaTransformerHandler.dequantize (LlamaTransformerHandler.java:873-1135). */
+int jh_qmat_dequant(jh_ctx *ctx, const jh_qmat *m, float *out);
+
+/* Plain fp32 GEMV with host operands, A[rows][cols] row-major; replaces
+ * MatVec.sgemv(float[] A, float[] x, rows, cols) (MatVec.java:56-66,
+ * RocmMatVec.java:138-197). */
+int jh_sgemv(jh_ctx *ctx, const float *A, const float *x, int rows, int cols, float *y);
+
+/* Device-pointer variants: operands already in HBM, enqueued on `stream`. */
+int jh_qmatvec_dev(const jh_qmat *m, const float *d_x, float *d_y, int row_start, int row_end,
+                   void *stream);
+int jh_qmatvec_batched_dev(const jh_qmat *m, const float *d_X, int B, float *d_Y, int row_start,
+                           int row_end, void *stream);
+int jh_qmat_dequant_dev(const jh_qmat *m, float *d_out, void *stream);
+
+/* Raw-pointer variant of the quantizer: n fp32 values -> packed bytes in a
+ * caller-provided device buffer of rawByteCount(type, n) bytes. */
+int jh_quantize_dev(int ggml_type, const float *d_src, int64_t n, void *d_dst, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* JUNOHIP_H */

@@ -1,0 +1,71 @@
+"""ctypes binding of libjunohip.so (the C ABI declared in include/junohip.h).
+
+The library is built in-tree (``python -m juno_amd.build``) and loaded from
+this package directory.  There is no fallback: if the library is missing,
+loading raises ``ImportError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libjunohip.so")
+
+JH_OK, JH_EINVAL, JH_ENOMEM, JH_EHIP, JH_EUNSUPPORTED, JH_ECLOSED, JH_ENODEV = range(7)
+
+# Every symbol include/junohip.h declares, with (restype, argtypes).
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+SIGNATURES = {
+    "jh_last_error": (ctypes.c_char_p, []),
+    "jh_version": (ctypes.c_char_p, []),
+    "jh_device_count": (_I, [ctypes.POINTER(_I)]),
+    "jh_device_info": (_I, [_I, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64), ctypes.c_char_p]),
+    "jh_ctx_create": (_I, [_I, ctypes.POINTER(_P)]),
+    "jh_ctx_destroy": (_I, [_P]),
+    "jh_raw_byte_count": (_I, [_I, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
+    "jh_qmat_upload": (_I, [_P, _I, _P, ctypes.c_size_t, _I, _I, ctypes.POINTER(_P)]),
+    "jh_qmat_quantize_dev": (_I, [_P, _I, _P, _I, _I, _P, ctypes.POINTER(_P)]),
+    "jh_qmat_free": (_I, [_P]),
+    "jh_qmat_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I),
+                          ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(_P)]),
+    "jh_qmatvec": (_I, [_P, _P, _P, _P, _I, _I]),
+    "jh_qmatvec_batched": (_I, [_P, _P, _P, _I, _P, _I, _I]),
+    "jh_qmat_dequant": (_I, [_P, _P, _P]),
+    "jh_sgemv": (_I, [_P, _P, _P, _I, _I, _P]),
+    "jh_qmatvec_dev": (_I, [_P, _P, _P, _I, _I, _P]),
+    "jh_qmatvec_batched_dev": (_I, [_P, _P, _I, _P, _I, _I, _P]),
+    "jh_qmat_dequant_dev": (_I, [_P, _P, _P]),
+    "jh_quantize_dev": (_I, [_I, _P, ctypes.c_int64, _P, _P]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libjunohip.so and declare its signatures; raise if it is absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run `python -m juno_amd.build` "
+                              "(the HIP library has no CPU fallback)")
+        # PyTorch-ROCm ships its own libamdhip64.so (soname libamdhip64.so.7)
+        # and its libraries request it by the unversioned name.  Loading torch
+        # first makes this library bind to that same runtime (same soname), so
+        # one process never holds two HIP runtimes.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return load().jh_last_error().decode("utf-8", "replace")

@@ -1,0 +1,39 @@
+"""Build libjunohip.so in-tree for gfx950 with hipcc.
+
+    python -m juno_amd.build
+
+Flags: -O3, C++17, and -Xclang -target-feature -Xclang -packed-fp32-ops, which keeps
+the compiler from emitting packed-fp32 VALU instructions.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "libjunohip.so")
+SOURCES = ["jh_api.cpp", "jh_gemv.hip", "jh_quant.hip", "jh_mfma.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-Wall",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def build(verbose: bool = False) -> str:
+    cmd = [HIPCC, *FLAGS, *[os.path.join(CSRC, s) for s in SOURCES], "-o", OUT + ".tmp"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    noise = ("packed-fp32-ops",)
+    errs = "\n".join(l for l in r.stderr.splitlines() if l.strip() and not any(n in l for n in noise))
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{errs}")
+    if errs and verbose:
+        print(errs, file=sys.stderr)
+    os.replace(OUT + ".tmp", OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

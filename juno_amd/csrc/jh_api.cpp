@@ -1,0 +1,471 @@
+// jh_api.cpp -- the C ABI of libjunohip.so (declared in include/junohip.h).
+//
+// Host-side runtime around the kernels: shared per-device contexts
+// (GpuContext.shared, GpuContext.java:109-120), device-resident packed
+// matrices (DeviceHalfMatrix, DeviceHalfMatrix.java:41-115), per-thread HIP
+// streams and pinned staging for the host-pointer calls (RocmMatVec's
+// ThreadLocal stream / scratch, RocmMatVec.java:64-92), argument validation
+// with the reference's messages, and a thread-local last-error string
+// (GpuBindings.check, GpuBindings.java:180-183).
+#include "../../include/junohip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "jh_kernels.hpp"
+
+struct jh_ctx {
+    int device;
+    int refs;
+    int cu_count;
+};
+
+struct jh_qmat {
+    jh_ctx *ctx;
+    int type, rows, cols;
+    size_t nbytes, pitch;
+    uint8_t *d_raw;  // owned; nbytes + kTailPad bytes
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return JH_OK;
+}
+
+int hip_fail(const char *op, hipError_t rc) {
+    return fail(JH_EHIP, "%s failed: rc=%d (%s)", op, (int)rc, hipGetErrorString(rc));
+}
+
+#define JH_HIP(op, expr)                                     \
+    do {                                                     \
+        hipError_t _rc = (expr);                             \
+        if (_rc != hipSuccess) return hip_fail((op), _rc);   \
+    } while (0)
+
+// Test hook: JUNO_HIP_FAIL_ALLOC_AFTER=N makes every device allocation after
+// the first N fail with JH_ENOMEM, so callers' CPU fallback can be exercised.
+std::atomic<long> g_alloc_count{0};
+
+long alloc_limit() {
+    static long limit = [] {
+        const char *v = getenv("JUNO_HIP_FAIL_ALLOC_AFTER");
+        return v ? atol(v) : -1L;
+    }();
+    return limit;
+}
+
+int device_alloc(void **p, size_t bytes) {
+    long lim = alloc_limit();
+    if (lim >= 0 && g_alloc_count.fetch_add(1) >= lim)
+        return fail(JH_ENOMEM, "hipMalloc failed: %zu bytes (JUNO_HIP_FAIL_ALLOC_AFTER=%ld)", bytes, lim);
+    hipError_t rc = hipMalloc(p, bytes);
+    if (rc != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(JH_ENOMEM, "hipMalloc failed: %zu bytes: rc=%d (%s)", bytes, (int)rc, hipGetErrorString(rc));
+    }
+    return JH_OK;
+}
+
+bool type_geometry(int type, int *qk, int *bb) {
+    switch (type) {
+    case JH_TYPE_F32: *qk = 1; *bb = 4; return true;
+    case JH_TYPE_Q8_0: *qk = 32; *bb = 34; return true;
+    case JH_TYPE_Q4_K: *qk = 256; *bb = 144; return true;
+    case JH_TYPE_Q6_K: *qk = 256; *bb = 210; return true;
+    default: return false;
+    }
+}
+
+// ---- shared contexts (one per device, reference counted)
+std::mutex g_ctx_mu;
+jh_ctx *g_ctx[64];
+
+// ---- per-thread, per-device stream and staging
+struct Staging {
+    hipStream_t stream = nullptr;
+    float *d_x = nullptr, *d_y = nullptr;
+    size_t cap_x = 0, cap_y = 0;
+    float *h_x = nullptr, *h_y = nullptr;  // pinned
+    size_t cap_hx = 0, cap_hy = 0;
+};
+
+struct ThreadStaging {
+    Staging per_dev[64];
+    ~ThreadStaging() {
+        for (auto &s : per_dev) {
+            if (s.d_x) (void)hipFree(s.d_x);
+            if (s.d_y) (void)hipFree(s.d_y);
+            if (s.h_x) (void)hipHostFree(s.h_x);
+            if (s.h_y) (void)hipHostFree(s.h_y);
+            if (s.stream) (void)hipStreamDestroy(s.stream);
+        }
+    }
+};
+thread_local ThreadStaging t_staging;
+
+int grow_dev(float **p, size_t *cap, size_t bytes) {
+    if (*cap >= bytes) return JH_OK;
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    int rc = device_alloc((void **)p, want);
+    if (rc) return rc;
+    *cap = want;
+    return JH_OK;
+}
+
+int grow_host(float **p, size_t *cap, size_t bytes) {
+    if (*cap >= bytes) return JH_OK;
+    if (*p) (void)hipHostFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    JH_HIP("hipHostMalloc(staging)", hipHostMalloc((void **)p, want, hipHostMallocDefault));
+    *cap = want;
+    return JH_OK;
+}
+
+int staging_for(int device, size_t bx, size_t by, Staging **out) {
+    Staging &s = t_staging.per_dev[device];
+    if (!s.stream) JH_HIP("hipStreamCreateWithFlags", hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
+    int rc;
+    if ((rc = grow_dev(&s.d_x, &s.cap_x, bx)) || (rc = grow_dev(&s.d_y, &s.cap_y, by)) ||
+        (rc = grow_host(&s.h_x, &s.cap_hx, bx)) || (rc = grow_host(&s.h_y, &s.cap_hy, by)))
+        return rc;
+    *out = &s;
+    return JH_OK;
+}
+
+int check_qmat(const jh_qmat *m) {
+    if (!m) return fail(JH_EINVAL, "A must not be null");
+    if (!m->d_raw) return fail(JH_ECLOSED, "DeviceQuantMatrix is closed");
+    return JH_OK;
+}
+
+int check_range(const jh_qmat *m, int row_start, int row_end) {
+    if (row_start < 0 || row_end < row_start || row_end > m->rows)
+        return fail(JH_EINVAL, "row range [%d, %d) outside rows=%d", row_start, row_end, m->rows);
+    return JH_OK;
+}
+
+// Enqueue y = W x for B vectors (device pointers), splitting B into the
+// kernel's supported batch widths, or using the MFMA path for B >= 16.
+int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int row_start, int row_end,
+                   hipStream_t s) {
+    const int nrows = row_end - row_start;
+    if (nrows == 0 || B == 0) return JH_OK;
+    jh::GemvArgs a;
+    a.type = m->type;
+    a.w = m->d_raw;
+    a.pitch = m->pitch;
+    a.cols = m->cols;
+    a.row_start = row_start;
+    a.row_end = row_end;
+    a.ldx = m->cols;
+    a.ldy = nrows;
+    if (B >= 16) {
+        a.batch = B;
+        a.x = d_x;
+        a.y = d_y;
+        hipError_t rc = jh::launch_gemm_mfma(a, s);
+        if (rc == hipSuccess) return JH_OK;
+        if (rc != hipErrorNotSupported) return hip_fail("gemm_mfma launch", rc);
+    }
+    int done = 0;
+    while (done < B) {
+        int left = B - done;
+        int w = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        a.batch = w;
+        a.x = d_x + (size_t)done * m->cols;
+        a.y = d_y + (size_t)done * nrows;
+        hipError_t rc = jh::launch_gemv(a, s);
+        if (rc != hipSuccess) return hip_fail("gemv launch", rc);
+        done += w;
+    }
+    return JH_OK;
+}
+
+int set_device(int dev) {
+    JH_HIP("hipSetDevice", hipSetDevice(dev));
+    return JH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *jh_last_error(void) { return g_last_error.c_str(); }
+
+const char *jh_version(void) { return "junohip 0.1 gfx950"; }
+
+int jh_device_count(int *count) {
+    if (!count) return fail(JH_EINVAL, "count must not be null");
+    int n = 0;
+    hipError_t rc = hipGetDeviceCount(&n);
+    if (rc != hipSuccess) {
+        (void)hipGetLastError();
+        *count = 0;
+        return ok();
+    }
+    *count = n;
+    return ok();
+}
+
+int jh_device_info(int device, char name[256], uint64_t *vram_bytes, char arch[64]) {
+    hipDeviceProp_t p;
+    JH_HIP("hipGetDeviceProperties", hipGetDeviceProperties(&p, device));
+    if (name) snprintf(name, 256, "%s", p.name);
+    if (vram_bytes) *vram_bytes = (uint64_t)p.totalGlobalMem;
+    if (arch) snprintf(arch, 64, "%s", p.gcnArchName);
+    return ok();
+}
+
+int jh_ctx_create(int device, jh_ctx **out) {
+    if (!out) return fail(JH_EINVAL, "out must not be null");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+        (void)hipGetLastError();
+        return fail(JH_ENODEV, "no HIP device available");
+    }
+    if (device < 0 || device >= n || device >= 64) return fail(JH_EINVAL, "device %d out of range (count=%d)", device, n);
+    hipDeviceProp_t p;
+    JH_HIP("hipGetDeviceProperties", hipGetDeviceProperties(&p, device));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(JH_ENODEV, "device %d is %s; libjunohip is built for gfx950 only", device, p.gcnArchName);
+    std::lock_guard<std::mutex> lk(g_ctx_mu);
+    if (!g_ctx[device]) {
+        int rc = set_device(device);
+        if (rc) return rc;
+        jh_ctx *c = new jh_ctx{device, 0, p.multiProcessorCount};
+        g_ctx[device] = c;
+    }
+    g_ctx[device]->refs++;
+    *out = g_ctx[device];
+    return ok();
+}
+
+int jh_ctx_destroy(jh_ctx *ctx) {
+    if (!ctx) return ok();
+    std::lock_guard<std::mutex> lk(g_ctx_mu);
+    // The shared context lives for the process, like GpuContext.shared; the
+    // count only tracks users.
+    if (ctx->refs > 0) ctx->refs--;
+    return ok();
+}
+
+int jh_raw_byte_count(int type, int64_t nelems, int64_t *out) {
+    int qk, bb;
+    if (!type_geometry(type, &qk, &bb)) return fail(JH_EUNSUPPORTED, "No byte-size formula for GGML type %d", type);
+    if (!out) return fail(JH_EINVAL, "out must not be null");
+    *out = (nelems / qk) * bb;
+    return ok();
+}
+
+static int qmat_alloc(jh_ctx *ctx, int type, int rows, int cols, jh_qmat **out) {
+    if (!ctx) return fail(JH_EINVAL, "ctx must not be null");
+    if (!out) return fail(JH_EINVAL, "out must not be null");
+    int qk, bb;
+    if (!type_geometry(type, &qk, &bb))
+        return fail(JH_EUNSUPPORTED, "Quantized matVec not implemented for GGML type %d", type);
+    if (rows < 0 || cols <= 0) return fail(JH_EINVAL, "rows*cols invalid: rows=%d cols=%d", rows, cols);
+    if (cols % qk) return fail(JH_EINVAL, "cols=%d is not a multiple of the block size %d", cols, qk);
+    int rc = set_device(ctx->device);
+    if (rc) return rc;
+    jh_qmat *m = new jh_qmat;
+    m->ctx = ctx;
+    m->type = type;
+    m->rows = rows;
+    m->cols = cols;
+    m->pitch = (size_t)(cols / qk) * bb;
+    m->nbytes = m->pitch * (size_t)rows;
+    m->d_raw = nullptr;
+    rc = device_alloc((void **)&m->d_raw, m->nbytes + jh::kTailPad);
+    if (rc) {
+        delete m;
+        return rc;
+    }
+    hipError_t e = hipMemset(m->d_raw + m->nbytes, 0, jh::kTailPad);
+    if (e != hipSuccess) {
+        (void)hipFree(m->d_raw);
+        delete m;
+        return hip_fail("hipMemset(pad)", e);
+    }
+    *out = m;
+    return JH_OK;
+}
+
+int jh_qmat_upload(jh_ctx *ctx, int type, const void *raw, size_t nbytes, int rows, int cols, jh_qmat **out) {
+    if (!raw && nbytes) return fail(JH_EINVAL, "raw must not be null");
+    int qk, bb;
+    if (type_geometry(type, &qk, &bb) && rows >= 0 && cols > 0 && cols % qk == 0) {
+        size_t want = (size_t)(cols / qk) * bb * (size_t)rows;
+        if (nbytes != want)
+            return fail(JH_EINVAL, "raw.length=%zu != rawByteCount(type=%d, rows*cols=%lld)=%zu", nbytes, type,
+                        (long long)rows * cols, want);
+    }
+    jh_qmat *m;
+    int rc = qmat_alloc(ctx, type, rows, cols, &m);
+    if (rc) return rc;
+    hipError_t e = hipMemcpy(m->d_raw, raw, nbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(m->d_raw);
+        delete m;
+        return hip_fail("hipMemcpy(raw H2D)", e);
+    }
+    *out = m;
+    return ok();
+}
+
+int jh_qmat_quantize_dev(jh_ctx *ctx, int type, const float *d_src, int rows, int cols, void *stream,
+                         jh_qmat **out) {
+    if (!d_src && rows) return fail(JH_EINVAL, "src must not be null");
+    jh_qmat *m;
+    int rc = qmat_alloc(ctx, type, rows, cols, &m);
+    if (rc) return rc;
+    hipError_t e = jh::launch_quantize(type, d_src, (int64_t)rows * cols, m->d_raw, (hipStream_t)stream);
+    if (e != hipSuccess) {
+        (void)hipFree(m->d_raw);
+        delete m;
+        return hip_fail("quantize launch", e);
+    }
+    *out = m;
+    return ok();
+}
+
+int jh_qmat_free(jh_qmat *m) {
+    if (!m) return ok();
+    if (m->d_raw) {
+        (void)hipSetDevice(m->ctx->device);
+        (void)hipFree(m->d_raw);
+    }
+    delete m;
+    return ok();
+}
+
+int jh_qmat_info(const jh_qmat *m, int *type, int *rows, int *cols, size_t *nbytes, const void **d_raw) {
+    if (!m) return fail(JH_EINVAL, "A must not be null");
+    if (type) *type = m->type;
+    if (rows) *rows = m->rows;
+    if (cols) *cols = m->cols;
+    if (nbytes) *nbytes = m->nbytes;
+    if (d_raw) *d_raw = m->d_raw;
+    return ok();
+}
+
+int jh_qmatvec_batched(jh_ctx *ctx, const jh_qmat *m, const float *X, int B, float *Y, int row_start, int row_end) {
+    int rc;
+    if (!ctx) return fail(JH_EINVAL, "ctx must not be null");
+    if ((rc = check_qmat(m)) || (rc = check_range(m, row_start, row_end))) return rc;
+    if (B < 0) return fail(JH_EINVAL, "B=%d must be >= 0", B);
+    if ((!X || !Y) && B > 0) return fail(JH_EINVAL, "x and y must not be null");
+    const int nrows = row_end - row_start;
+    if (B == 0 || nrows == 0) return ok();
+    if ((rc = set_device(ctx->device))) return rc;
+    const size_t bx = (size_t)B * m->cols * 4, by = (size_t)B * nrows * 4;
+    Staging *s;
+    if ((rc = staging_for(ctx->device, bx, by, &s))) return rc;
+    memcpy(s->h_x, X, bx);
+    JH_HIP("hipMemcpyAsync(x H2D)", hipMemcpyAsync(s->d_x, s->h_x, bx, hipMemcpyHostToDevice, s->stream));
+    if ((rc = enqueue_matvec(m, s->d_x, B, s->d_y, row_start, row_end, s->stream))) return rc;
+    JH_HIP("hipMemcpyAsync(y D2H)", hipMemcpyAsync(s->h_y, s->d_y, by, hipMemcpyDeviceToHost, s->stream));
+    JH_HIP("hipStreamSynchronize", hipStreamSynchronize(s->stream));
+    memcpy(Y, s->h_y, by);
+    return ok();
+}
+
+int jh_qmatvec(jh_ctx *ctx, const jh_qmat *m, const float *x, float *y, int row_start, int row_end) {
+    return jh_qmatvec_batched(ctx, m, x, 1, y, row_start, row_end);
+}
+
+int jh_qmat_dequant(jh_ctx *ctx, const jh_qmat *m, float *out) {
+    int rc;
+    if (!ctx) return fail(JH_EINVAL, "ctx must not be null");
+    if ((rc = check_qmat(m))) return rc;
+    if (!out && m->rows) return fail(JH_EINVAL, "out must not be null");
+    if ((rc = set_device(ctx->device))) return rc;
+    const size_t bytes = (size_t)m->rows * m->cols * 4;
+    if (bytes == 0) return ok();
+    float *d_out = nullptr;
+    if ((rc = device_alloc((void **)&d_out, bytes))) return rc;
+    Staging *s;
+    if ((rc = staging_for(ctx->device, 0, 0, &s))) {
+        (void)hipFree(d_out);
+        return rc;
+    }
+    hipError_t e = jh::launch_dequant(m->type, m->d_raw, m->rows, m->cols, d_out, s->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, d_out, bytes, hipMemcpyDeviceToHost, s->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+    (void)hipFree(d_out);
+    if (e != hipSuccess) return hip_fail("dequant", e);
+    return ok();
+}
+
+int jh_sgemv(jh_ctx *ctx, const float *A, const float *x, int rows, int cols, float *y) {
+    // MatVec contract (MatVec.java:46-54, MatVecBackendContractTest.java:196-212).
+    if (!ctx) return fail(JH_EINVAL, "ctx must not be null");
+    if (rows < 0 || cols <= 0) return fail(JH_EINVAL, "invalid shape: rows*cols with rows=%d cols=%d", rows, cols);
+    if (!A || !x || !y) return fail(JH_EINVAL, "A, x and y must not be null");
+    jh_qmat *m;
+    int rc = jh_qmat_upload(ctx, JH_TYPE_F32, A, (size_t)rows * cols * 4, rows, cols, &m);
+    if (rc) return rc;
+    rc = jh_qmatvec(ctx, m, x, y, 0, rows);
+    std::string err = g_last_error;
+    jh_qmat_free(m);
+    g_last_error = err;
+    return rc;
+}
+
+int jh_qmatvec_dev(const jh_qmat *m, const float *d_x, float *d_y, int row_start, int row_end, void *stream) {
+    return jh_qmatvec_batched_dev(m, d_x, 1, d_y, row_start, row_end, stream);
+}
+
+int jh_qmatvec_batched_dev(const jh_qmat *m, const float *d_X, int B, float *d_Y, int row_start, int row_end,
+                           void *stream) {
+    int rc;
+    if ((rc = check_qmat(m)) || (rc = check_range(m, row_start, row_end))) return rc;
+    if (B < 0) return fail(JH_EINVAL, "B=%d must be >= 0", B);
+    if ((!d_X || !d_Y) && B > 0 && row_end > row_start) return fail(JH_EINVAL, "x and y must not be null");
+    if ((rc = enqueue_matvec(m, d_X, B, d_Y, row_start, row_end, (hipStream_t)stream))) return rc;
+    return ok();
+}
+
+int jh_qmat_dequant_dev(const jh_qmat *m, float *d_out, void *stream) {
+    int rc;
+    if ((rc = check_qmat(m))) return rc;
+    hipError_t e = jh::launch_dequant(m->type, m->d_raw, m->rows, m->cols, d_out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("dequant launch", e);
+    return ok();
+}
+
+int jh_quantize_dev(int type, const float *d_src, int64_t n, void *d_dst, void *stream) {
+    int qk, bb;
+    if (!type_geometry(type, &qk, &bb)) return fail(JH_EUNSUPPORTED, "Re-quantisation not implemented for GGML type %d", type);
+    if (n < 0 || n % qk) return fail(JH_EINVAL, "n=%lld is not a multiple of the block size %d", (long long)n, qk);
+    hipError_t e = jh::launch_quantize(type, d_src, n, (uint8_t *)d_dst, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("quantize launch", e);
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,353 @@
+// jh_gemv.hip -- fused dequant-GEMV kernels for gfx950 on packed GGUF blocks.
+//
+// y[j][r] = sum_c deq(W[r][c]) * x[j][c] for a small batch of B vectors
+// (B = 1 is the decode GEMV).  The weights are streamed from HBM exactly once
+// in their packed layout; dequantization happens in registers.
+//
+// Work split (all three quantized kernels): a workgroup is 4 wavefronts, a
+// wavefront owns R consecutive rows, and its 64 lanes sweep the row's blocks
+// as 8 blocks x 8 lanes per step.  All R rows share each lane's x values, so
+// x is read R times less than the weights would require.  Per-lane partial
+// sums are reduced with DPP (jh::wave_sum).
+//
+// Numerics.  The Java path (LlamaTransformerHandler.java:1428-1468,
+// 1486-1508, 1587-1638) sums (scale*q - min)*x per element in fp32.  Here
+// each sub-block is folded as  scale * sum(q*x) - min * sum(x)  (fp32 FMAs),
+// which is the same sum in another order; the difference is order-of-
+// summation rounding only (bar: max rel-err 1e-3 against the Java path).
+#include "jh_device.hpp"
+#include "jh_kernels.hpp"
+
+namespace jh {
+
+// ---------------------------------------------------------------- Q4_K
+// Lane (kb, ch): block b = step*8 + kb, 16-byte qs chunk ch of that block.
+// Chunk ch covers group g = ch/2, elements 16*(ch&1) .. +16 of sub-block 2g
+// (low nibbles) and of sub-block 2g+1 (high nibbles).
+template <int R, int B>
+__global__ __launch_bounds__(256) void gemv_q4k(const uint8_t *__restrict__ W, size_t pitch, int nb,
+                                                int nrows, const float *__restrict__ X, int ldx,
+                                                float *__restrict__ Y, int ldy) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * 4 + wave) * R;
+    if (r0 >= nrows) return;
+    const int kb = lane >> 3, ch = lane & 7, g = ch >> 1, hf = ch & 1;
+
+    float acc[R][B];
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) acc[i][j] = 0.f;
+
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) rowp[i] = W + (size_t)min(r0 + i, nrows - 1) * pitch;
+
+    for (int b = kb; b < nb; b += 8) {
+        uint4 hdr[R], qs[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const uint8_t *bp = rowp[i] + (size_t)b * 144;
+            hdr[i] = *reinterpret_cast<const uint4 *>(bp);
+            qs[i] = load_stream16(bp + 16 + ch * 16);
+        }
+        const int xo = b * 256 + g * 64 + hf * 16;
+        float xl[B][16], xh[B][16], sl[B], sh[B];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const float *xp = X + (size_t)j * ldx + xo;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float4 a = load_f4(xp + 4 * k), c = load_f4(xp + 32 + 4 * k);
+                xl[j][4 * k] = a.x; xl[j][4 * k + 1] = a.y; xl[j][4 * k + 2] = a.z; xl[j][4 * k + 3] = a.w;
+                xh[j][4 * k] = c.x; xh[j][4 * k + 1] = c.y; xh[j][4 * k + 2] = c.z; xh[j][4 * k + 3] = c.w;
+            }
+            float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; k++) { s0 += xl[j][k]; s1 += xh[j][k]; }
+            sl[j] = s0;
+            sh[j] = s1;
+        }
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const float d = half_bits_to_float(hdr[i].x), dmin = half_bits_to_float(hdr[i].x >> 16);
+            int ls0, lm0, ls1, lm1;
+            q4k_scale_min(hdr[i].y, hdr[i].z, hdr[i].w, 2 * g, ls0, lm0);
+            q4k_scale_min(hdr[i].y, hdr[i].z, hdr[i].w, 2 * g + 1, ls1, lm1);
+            const float sc0 = d * (float)ls0, mn0 = dmin * (float)lm0;
+            const float sc1 = d * (float)ls1, mn1 = dmin * (float)lm1;
+            const uint32_t w[4] = {qs[i].x, qs[i].y, qs[i].z, qs[i].w};
+#pragma unroll
+            for (int j = 0; j < B; j++) {
+                float dl = 0.f, dh = 0.f;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t lo = w[k] & 0x0F0F0F0Fu, hi = (w[k] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        dl = fmaf((float)byte_of(lo, e), xl[j][4 * k + e], dl);
+                        dh = fmaf((float)byte_of(hi, e), xh[j][4 * k + e], dh);
+                    }
+                }
+                float a = acc[i][j];
+                a = fmaf(sc0, dl, a);
+                a = fmaf(-mn0, sl[j], a);
+                a = fmaf(sc1, dh, a);
+                a = fmaf(-mn1, sh[j], a);
+                acc[i][j] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            float s = wave_sum(acc[i][j]);
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+        }
+}
+
+// ---------------------------------------------------------------- Q6_K
+// Lane (kb, ch): block b = step*8 + kb; half h = ch/4, l0 = 8*(ch&3).  The lane
+// covers l in [l0, l0+8) of that half for all four quads (elements l, l+32,
+// l+64, l+96), i.e. 32 weights, reading 8 bytes each of ql[l], ql[l+32], qh[l].
+template <int R, int B>
+__global__ __launch_bounds__(256) void gemv_q6k(const uint8_t *__restrict__ W, size_t pitch, int nb,
+                                                int nrows, const float *__restrict__ X, int ldx,
+                                                float *__restrict__ Y, int ldy) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * 4 + wave) * R;
+    if (r0 >= nrows) return;
+    const int kb = lane >> 3, ch = lane & 7, h = ch >> 2, l0 = (ch & 3) * 8, is = l0 >> 4;
+
+    float acc[R][B];
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) acc[i][j] = 0.f;
+
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) rowp[i] = W + (size_t)min(r0 + i, nrows - 1) * pitch;
+
+    for (int b = kb; b < nb; b += 8) {
+        uint2 qa[R], qb[R], qh[R], scw[R];
+        uint32_t dw[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const uint8_t *bp = rowp[i] + (size_t)b * 210;
+            qa[i] = load8_a2(bp + h * 64 + l0);
+            qb[i] = load8_a2(bp + h * 64 + 32 + l0);
+            qh[i] = load8_a2(bp + 128 + h * 32 + l0);
+            scw[i] = load8_a2(bp + 192 + h * 8);
+            const uint8_t *dp = bp + 208;
+            uintptr_t a = reinterpret_cast<uintptr_t>(dp);
+            uint32_t w = *reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+            dw[i] = w >> (8 * (a & 3u));
+        }
+        // x runs for quads k = 0..3: x[b*256 + h*128 + k*32 + l0 .. +8]
+        float xv[B][4][8], sx[B][4];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const float *xp = X + (size_t)j * ldx + b * 256 + h * 128 + l0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float4 a = load_f4(xp + 32 * k), c = load_f4(xp + 32 * k + 4);
+                xv[j][k][0] = a.x; xv[j][k][1] = a.y; xv[j][k][2] = a.z; xv[j][k][3] = a.w;
+                xv[j][k][4] = c.x; xv[j][k][5] = c.y; xv[j][k][6] = c.z; xv[j][k][7] = c.w;
+                float s = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) s += xv[j][k][e];
+                sx[j][k] = s;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const float d = half_bits_to_float(dw[i]);
+            // scales sc[h*8 + is + 2k], k = 0..3 (signed bytes)
+            float dk[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int idx = is + 2 * k;
+                const uint32_t word = idx < 4 ? scw[i].x : scw[i].y;
+                const int s8 = (int)(int8_t)byte_of(word, idx & 3);
+                dk[k] = d * (float)s8;
+            }
+            uint32_t u[4][2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const uint32_t a = t ? qa[i].y : qa[i].x, c = t ? qb[i].y : qb[i].x, e = t ? qh[i].y : qh[i].x;
+                u[0][t] = (a & 0x0F0F0F0Fu) | ((e << 4) & 0x30303030u);
+                u[1][t] = (c & 0x0F0F0F0Fu) | ((e << 2) & 0x30303030u);
+                u[2][t] = ((a >> 4) & 0x0F0F0F0Fu) | (e & 0x30303030u);
+                u[3][t] = ((c >> 4) & 0x0F0F0F0Fu) | ((e >> 2) & 0x30303030u);
+            }
+#pragma unroll
+            for (int j = 0; j < B; j++) {
+                float a = acc[i][j];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    float dot = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        dot = fmaf((float)byte_of(u[k][e >> 2], e & 3), xv[j][k][e], dot);
+                    // q = u - 32
+                    a = fmaf(dk[k], fmaf(-32.f, sx[j][k], dot), a);
+                }
+                acc[i][j] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            float s = wave_sum(acc[i][j]);
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+        }
+}
+
+// ---------------------------------------------------------------- Q8_0
+// One lane per 34-byte block (32 weights); a wavefront step covers 64 blocks.
+// The block start is 2-byte aligned: ten aligned dwords cover it.
+template <int R, int B>
+__global__ __launch_bounds__(256) void gemv_q8_0(const uint8_t *__restrict__ W, size_t pitch, int nb,
+                                                 int nrows, const float *__restrict__ X, int ldx,
+                                                 float *__restrict__ Y, int ldy) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r0 = (blockIdx.x * 4 + wave) * R;
+    if (r0 >= nrows) return;
+
+    float acc[R][B];
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) acc[i][j] = 0.f;
+
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) rowp[i] = W + (size_t)min(r0 + i, nrows - 1) * pitch;
+
+    for (int b = lane; b < nb; b += 64) {
+        uint32_t q[R][8];
+        float dsc[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const uintptr_t a = reinterpret_cast<uintptr_t>(rowp[i] + (size_t)b * 34);
+            const uint32_t *w = reinterpret_cast<const uint32_t *>(a & ~uintptr_t(3));
+            const uint32_t mis = (uint32_t)(a & 3u);  // 0 or 2
+            uint32_t v[10];
+            u32x4a4 v0 = *reinterpret_cast<const u32x4a4 *>(w);
+            u32x4a4 v1 = *reinterpret_cast<const u32x4a4 *>(w + 4);
+            u32x2a4 v2 = *reinterpret_cast<const u32x2a4 *>(w + 8);
+            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+            v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+            v[8] = v2.x; v[9] = v2.y;
+            dsc[i] = half_bits_to_float(mis ? (v[0] >> 16) : v[0]);
+            // q bytes start at byte offset mis + 2 of the window
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t lo = mis ? v[k + 1] : v[k], hi = mis ? v[k + 2] : v[k + 1];
+                // flip the sign bits: byte value u = q + 128
+                q[i][k] = __builtin_amdgcn_alignbyte(hi, lo, mis ? 0u : 2u) ^ 0x80808080u;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const float *xp = X + (size_t)j * ldx + b * 32;
+            float xv[32];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                float4 a = load_f4(xp + 4 * k);
+                xv[4 * k] = a.x; xv[4 * k + 1] = a.y; xv[4 * k + 2] = a.z; xv[4 * k + 3] = a.w;
+            }
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < 32; k++) s += xv[k];
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                float dot = 0.f;
+#pragma unroll
+                for (int k = 0; k < 32; k++) dot = fmaf((float)byte_of(q[i][k >> 2], k & 3), xv[k], dot);
+                acc[i][j] = fmaf(dsc[i], fmaf(-128.f, s, dot), acc[i][j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            float s = wave_sum(acc[i][j]);
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+        }
+}
+
+// ---------------------------------------------------------------- F32
+// One wavefront per row; lanes stride along the row.
+template <int B>
+__global__ __launch_bounds__(256) void gemv_f32(const float *__restrict__ W, size_t ld, int cols, int nrows,
+                                                const float *__restrict__ X, int ldx, float *__restrict__ Y,
+                                                int ldy) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + wave;
+    if (r >= nrows) return;
+    const float *wr = W + (size_t)r * ld;
+    float acc[B];
+#pragma unroll
+    for (int j = 0; j < B; j++) acc[j] = 0.f;
+    for (int c = lane; c < cols; c += 64) {
+        const float w = __builtin_nontemporal_load(wr + c);
+#pragma unroll
+        for (int j = 0; j < B; j++) acc[j] = fmaf(w, X[(size_t)j * ldx + c], acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < B; j++) {
+        float s = wave_sum(acc[j]);
+        if (lane == 0) Y[(size_t)j * ldy + r] = s;
+    }
+}
+
+// ---------------------------------------------------------------- launchers
+
+template <int R, int B>
+static hipError_t launch_q(int type, const uint8_t *W, size_t pitch, int nb, int nrows, const float *X, int ldx,
+                           float *Y, int ldy, hipStream_t s) {
+    const int rows_per_wg = 4 * R;
+    dim3 grid((nrows + rows_per_wg - 1) / rows_per_wg), block(256);
+    switch (type) {
+    case 12: gemv_q4k<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
+    case 14: gemv_q6k<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
+    case 8: gemv_q8_0<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int B>
+static hipError_t launch_b(const GemvArgs &a, hipStream_t s) {
+    const uint8_t *W = a.w + (size_t)a.row_start * a.pitch;
+    const int nrows = a.row_end - a.row_start;
+    if (a.type == 0) {
+        dim3 grid((nrows + 3) / 4), block(256);
+        gemv_f32<B><<<grid, block, 0, s>>>(reinterpret_cast<const float *>(W), a.pitch / 4, a.cols, nrows, a.x,
+                                          a.ldx, a.y, a.ldy);
+        return hipGetLastError();
+    }
+    const int nb = a.type == 8 ? a.cols / 32 : a.cols / 256;
+    // Two rows per wavefront share x; one row when that leaves too few waves.
+    if (B <= 2 && nrows >= 2048)
+        return launch_q<2, B>(a.type, W, a.pitch, nb, nrows, a.x, a.ldx, a.y, a.ldy, s);
+    return launch_q<1, B>(a.type, W, a.pitch, nb, nrows, a.x, a.ldx, a.y, a.ldy, s);
+}
+
+hipError_t launch_gemv(const GemvArgs &a, hipStream_t s) {
+    switch (a.batch) {
+    case 1: return launch_b<1>(a, s);
+    case 2: return launch_b<2>(a, s);
+    case 4: return launch_b<4>(a, s);
+    case 8: return launch_b<8>(a, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace jh

@@ -1,0 +1,40 @@
+// jh_kernels.hpp -- host-side launch interface of the libjunohip kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace jh {
+
+// Bytes of zero padding after every packed matrix: the kernels read whole
+// aligned dwords around 2-byte-aligned Q6_K / Q8_0 fields, which can reach up
+// to 6 bytes past the last block.
+constexpr size_t kTailPad = 256;
+
+struct GemvArgs {
+    int type;        // ggml type: 0, 8, 12, 14
+    const uint8_t *w;  // packed matrix base (row 0)
+    size_t pitch;    // bytes per row
+    int cols;
+    int row_start, row_end;
+    int batch;       // 1, 2, 4 or 8 right-hand sides
+    const float *x;  // x[j][cols], j < batch, stride ldx floats
+    int ldx;
+    float *y;        // y[j][row_end-row_start], stride ldy floats
+    int ldy;
+};
+
+hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
+
+// Batched decode through the LDS-dequant + fp16 MFMA path (B >= 16).
+// Returns hipErrorNotSupported for types without an MFMA kernel.
+hipError_t launch_gemm_mfma(const GemvArgs &a, hipStream_t s);
+
+// out[rows][cols] fp32, bit-exact with the reference dequantizers.
+hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float *out, hipStream_t s);
+
+// n fp32 values -> packed blocks with the LoraMerge quantizers.
+hipError_t launch_quantize(int type, const float *src, int64_t n, uint8_t *dst, hipStream_t s);
+
+}  // namespace jh

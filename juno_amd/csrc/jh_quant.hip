@@ -1,0 +1,271 @@
+// jh_quant.hip -- dequantization (bit-exact) and quantization kernels.
+//
+// Dequantization restates LlamaTransformerHandler.dequantize
+// (LlamaTransformerHandler.java:873-1135).  Every product there is exact in
+// fp32 (an 11-bit fp16 significand times a 6- or 8-bit scale times a 4-, 6- or
+// 8-bit quant), so only the Q4_K "- min" rounds; the explicit _rn intrinsics
+// keep each step a separately rounded IEEE operation anyway.
+//
+// Quantization restates LoraMerge.requantize (LoraMerge.java:226-469) so that
+// benchmark and test inputs are the reference quantizer's bytes, produced on
+// the device.  One thread per block: the reference is sequential per block and
+// its rounding (Math.round, fp32 divisions) is reproduced exactly.
+#include "jh_device.hpp"
+#include "jh_kernels.hpp"
+
+namespace jh {
+
+// ---------------------------------------------------------------- dequant
+
+__global__ void dequant_q4k(const uint8_t *__restrict__ W, int64_t nsub, float *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 32-element sub-block
+    if (t >= nsub) return;
+    const int64_t blk = t >> 3;
+    const int j = (int)(t & 7), g = j >> 1;
+    const uint8_t *bp = W + blk * 144;
+    const float d = half_bits_to_float(bp[0] | (bp[1] << 8));
+    const float dmin = half_bits_to_float(bp[2] | (bp[3] << 8));
+    const uint32_t s0 = bp[4] | (bp[5] << 8) | (bp[6] << 16) | ((uint32_t)bp[7] << 24);
+    const uint32_t s1 = bp[8] | (bp[9] << 8) | (bp[10] << 16) | ((uint32_t)bp[11] << 24);
+    const uint32_t s2 = bp[12] | (bp[13] << 8) | (bp[14] << 16) | ((uint32_t)bp[15] << 24);
+    int ls, lm;
+    q4k_scale_min(s0, s1, s2, j, ls, lm);
+    const float scale = __fmul_rn(d, (float)ls), mn = __fmul_rn(dmin, (float)lm);
+    const uint8_t *qs = bp + 16 + g * 32;
+    const int shift = (j & 1) * 4;
+    float *o = out + t * 32;
+    for (int i = 0; i < 32; i++) o[i] = __fsub_rn(__fmul_rn(scale, (float)((qs[i] >> shift) & 0x0F)), mn);
+}
+
+__global__ void dequant_q6k(const uint8_t *__restrict__ W, int64_t nsub, float *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 16-element sub-block
+    if (t >= nsub) return;
+    const int64_t blk = t >> 4;
+    const int s = (int)(t & 15), half = s >> 3, k = (s & 7) >> 1, is = s & 1;
+    const uint8_t *bp = W + blk * 210;
+    const float d = half_bits_to_float(bp[208] | (bp[209] << 8));
+    const float dk = __fmul_rn(d, (float)(int8_t)bp[192 + half * 8 + is + 2 * k]);
+    const uint8_t *ql = bp + half * 64 + ((k & 1) ? 32 : 0);
+    const uint8_t *qh = bp + 128 + half * 32;
+    const int nsh = (k >> 1) * 4, hsh = 2 * k;
+    float *o = out + blk * 256 + half * 128 + k * 32 + is * 16;
+    for (int i = 0; i < 16; i++) {
+        const int l = is * 16 + i;
+        const int q = (((ql[l] >> nsh) & 0x0F) | (((qh[l] >> hsh) & 3) << 4)) - 32;
+        o[i] = __fmul_rn(dk, (float)q);
+    }
+}
+
+__global__ void dequant_q8_0(const uint8_t *__restrict__ W, int64_t nblk, float *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk) return;
+    const uint8_t *bp = W + t * 34;
+    const float d = half_bits_to_float(bp[0] | (bp[1] << 8));
+    float *o = out + t * 32;
+    for (int i = 0; i < 32; i++) o[i] = __fmul_rn(d, (float)(int8_t)bp[2 + i]);
+}
+
+__global__ void copy_f32(const float *__restrict__ W, int64_t n, float *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < n) out[t] = W[t];
+}
+
+hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float *out, hipStream_t s) {
+    const int64_t n = (int64_t)rows * cols;
+    int64_t units;
+    switch (type) {
+    case 12: units = n / 32; break;
+    case 14: units = n / 16; break;
+    case 8: units = n / 32; break;
+    case 0: units = n; break;
+    default: return hipErrorInvalidValue;
+    }
+    if (units == 0) return hipSuccess;
+    dim3 block(256), grid((unsigned)((units + 255) / 256));
+    switch (type) {
+    case 12: dequant_q4k<<<grid, block, 0, s>>>(w, units, out); break;
+    case 14: dequant_q6k<<<grid, block, 0, s>>>(w, units, out); break;
+    case 8: dequant_q8_0<<<grid, block, 0, s>>>(w, units, out); break;
+    case 0: copy_f32<<<grid, block, 0, s>>>(reinterpret_cast<const float *>(w), units, out); break;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- quantize
+
+// java.lang.Math.round(float): floor(a + 0.5) exactly (a + 0.5 is exact in
+// double), NaN -> 0, saturating.
+__device__ __forceinline__ int java_round(float a) {
+    if (a != a) return 0;
+    const double r = floor(__dadd_rn((double)a, 0.5));
+    if (r >= 2147483647.0) return 2147483647;
+    if (r <= -2147483648.0) return (int)0x80000000u;
+    return (int)r;
+}
+
+__device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// LoraMerge.f32ToF16 (LoraMerge.java:589-605): round-to-nearest-even on the
+// normal range; NaN becomes infinity; the subnormal branch rounds after a
+// truncating shift.  Reproduced as-is so the stored d / dmin bytes match.
+__device__ uint32_t f32_to_f16_ref(float value) {
+    const int32_t bits = __builtin_bit_cast(int32_t, value);
+    const int32_t sign = (int32_t)(((uint32_t)bits >> 31) & 1u);
+    int32_t exp = (int32_t)(((uint32_t)bits >> 23) & 0xFFu) - 112;
+    int32_t mant = bits & 0x7FFFFF;
+    if (exp <= 0) {
+        if (exp < -10) return (uint32_t)(sign << 15);
+        mant = (mant | 0x800000) >> (1 - exp);
+        mant = (mant + 0x0FFF + ((mant >> 13) & 1)) >> 13;
+        return (uint32_t)((sign << 15) | mant);
+    }
+    if (exp >= 31) return (uint32_t)((sign << 15) | 0x7C00);
+    const int32_t low = mant & 0x1FFF;
+    mant >>= 13;
+    if (low > 0x1000 || (low == 0x1000 && (mant & 1))) {
+        mant++;
+        if (mant == 0x400) {
+            mant = 0;
+            exp++;
+        }
+    }
+    if (exp >= 31) return (uint32_t)((sign << 15) | 0x7C00);
+    return (uint32_t)((sign << 15) | (exp << 10) | mant);
+}
+
+__device__ __forceinline__ void put16(uint8_t *p, uint32_t v) {
+    p[0] = (uint8_t)(v & 0xFF);
+    p[1] = (uint8_t)(v >> 8);
+}
+
+// quantizeQ8_0 (LoraMerge.java:265-277)
+__global__ void quant_q8_0(const float *__restrict__ src, int64_t nblk, uint8_t *__restrict__ dst) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk) return;
+    const float *v = src + t * 32;
+    uint8_t *o = dst + t * 34;
+    float absMax = 0.f;
+    for (int i = 0; i < 32; i++) absMax = fmaxf(absMax, fabsf(v[i]));
+    const float d = __fdiv_rn(absMax, 127.f);
+    const float invD = d > 0.f ? __fdiv_rn(1.f, d) : 0.f;
+    put16(o, f32_to_f16_ref(d));
+    for (int i = 0; i < 32; i++) o[2 + i] = (uint8_t)(int8_t)clampi(java_round(__fmul_rn(v[i], invD)), -127, 127);
+}
+
+// quantizeQ4_K (LoraMerge.java:311-366); the nibbles use the fp32 d / dmin.
+__global__ void quant_q4k(const float *__restrict__ src, int64_t nblk, uint8_t *__restrict__ dst) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk) return;
+    const float *v = src + t * 256;
+    uint8_t *o = dst + t * 144;
+    float mins[8], ranges[8];
+    for (int s = 0; s < 8; s++) {
+        float mn = 3.40282347e+38f, mx = -3.40282347e+38f;
+        for (int i = 0; i < 32; i++) {
+            const float e = v[s * 32 + i];
+            if (e < mn) mn = e;
+            if (e > mx) mx = e;
+        }
+        if (mn > mx) {
+            mn = 0.f;
+            mx = 0.f;
+        }
+        mins[s] = mn;
+        ranges[s] = __fsub_rn(mx, mn);
+    }
+    float maxRange = 0.f, maxAbsMin = 0.f;
+    for (int s = 0; s < 8; s++) {
+        if (ranges[s] > maxRange) maxRange = ranges[s];
+        const float am = -mins[s];
+        if (am > maxAbsMin) maxAbsMin = am;
+    }
+    const float d = maxRange > 0.f ? __fdiv_rn(maxRange, 945.f) : 0.f;
+    const float dmin = maxAbsMin > 0.f ? __fdiv_rn(maxAbsMin, 63.f) : 0.f;
+    int ls[8], lm[8];
+    for (int s = 0; s < 8; s++) {
+        ls[s] = maxRange > 0.f ? clampi(java_round(__fdiv_rn(__fmul_rn(ranges[s], 63.f), maxRange)), 0, 63) : 0;
+        lm[s] = maxAbsMin > 0.f ? clampi(java_round(__fdiv_rn(__fmul_rn(-mins[s], 63.f), maxAbsMin)), 0, 63) : 0;
+    }
+    put16(o, f32_to_f16_ref(d));
+    put16(o + 2, f32_to_f16_ref(dmin));
+    for (int j = 0; j < 4; j++) {
+        o[4 + j] = (uint8_t)((ls[j] & 0x3F) | ((ls[j + 4] & 0x30) << 2));
+        o[8 + j] = (uint8_t)((lm[j] & 0x3F) | ((lm[j + 4] & 0x30) << 2));
+        o[12 + j] = (uint8_t)((ls[j + 4] & 0x0F) | ((lm[j + 4] & 0x0F) << 4));
+    }
+    for (int g = 0; g < 4; g++) {
+        const int s0 = 2 * g, s1 = s0 + 1;
+        const float sc0 = __fmul_rn(d, (float)ls[s0]), mn0 = __fmul_rn(dmin, (float)lm[s0]);
+        const float sc1 = __fmul_rn(d, (float)ls[s1]), mn1 = __fmul_rn(dmin, (float)lm[s1]);
+        for (int i = 0; i < 32; i++) {
+            const int q0 = sc0 > 0.f ? clampi(java_round(__fdiv_rn(__fadd_rn(v[s0 * 32 + i], mn0), sc0)), 0, 15) : 0;
+            const int q1 = sc1 > 0.f ? clampi(java_round(__fdiv_rn(__fadd_rn(v[s1 * 32 + i], mn1), sc1)), 0, 15) : 0;
+            o[16 + g * 32 + i] = (uint8_t)(q0 | (q1 << 4));
+        }
+    }
+}
+
+// quantizeQ6_K (LoraMerge.java:437-469)
+__global__ void quant_q6k(const float *__restrict__ src, int64_t nblk, uint8_t *__restrict__ dst) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk) return;
+    const float *v = src + t * 256;
+    uint8_t *o = dst + t * 210;
+    float subMax[16];
+    float globalMax = 0.f;
+    for (int s = 0; s < 16; s++) {
+        float m = 0.f;
+        for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[s * 16 + i]));
+        subMax[s] = m;
+        if (m > globalMax) globalMax = m;
+    }
+    const float d = globalMax > 0.f ? __fdiv_rn(globalMax, 4064.f) : 0.f;
+    const float invD = d > 0.f ? __fdiv_rn(1.f, d) : 0.f;
+    int sc[16];
+    for (int s = 0; s < 16; s++) {
+        sc[s] = d > 0.f ? clampi(java_round(__fdiv_rn(__fmul_rn(subMax[s], invD), 32.f)), -127, 127) : 0;
+        o[192 + s] = (uint8_t)(int8_t)sc[s];
+    }
+    // Each ql / qh byte is assembled from the elements it encodes; the result
+    // equals the reference's read-modify-write loop over elements p.
+    auto u_of = [&](int p) {
+        const int half = p >> 7, lp = p & 127, quad = lp >> 5, l = lp & 31;
+        const int sub = half * 8 + (l >> 4) + quad * 2;
+        const float eff = __fmul_rn(d, (float)sc[sub]);
+        const int q6 = eff != 0.f ? clampi(java_round(__fdiv_rn(v[p], eff)), -32, 31) : 0;
+        return q6 + 32;
+    };
+    for (int idx = 0; idx < 128; idx++) {
+        const int half = idx >> 6, odd = (idx >> 5) & 1, l = idx & 31;
+        const int lo = u_of(half * 128 + odd * 32 + l), hi = u_of(half * 128 + (odd + 2) * 32 + l);
+        o[idx] = (uint8_t)((lo & 0x0F) | ((hi & 0x0F) << 4));
+    }
+    for (int idx = 0; idx < 64; idx++) {
+        const int half = idx >> 5, l = idx & 31;
+        uint32_t b = 0;
+        for (int quad = 0; quad < 4; quad++) b |= (uint32_t)((u_of(half * 128 + quad * 32 + l) >> 4) & 3) << (2 * quad);
+        o[128 + idx] = (uint8_t)b;
+    }
+    put16(o + 208, f32_to_f16_ref(d));
+}
+
+hipError_t launch_quantize(int type, const float *src, int64_t n, uint8_t *dst, hipStream_t s) {
+    int64_t nblk;
+    switch (type) {
+    case 8: nblk = n / 32; break;
+    case 12:
+    case 14: nblk = n / 256; break;
+    case 0: return hipMemcpyAsync(dst, src, (size_t)n * 4, hipMemcpyDeviceToDevice, s);
+    default: return hipErrorInvalidValue;
+    }
+    if (nblk == 0) return hipSuccess;
+    dim3 block(128), grid((unsigned)((nblk + 127) / 128));
+    switch (type) {
+    case 8: quant_q8_0<<<grid, block, 0, s>>>(src, nblk, dst); break;
+    case 12: quant_q4k<<<grid, block, 0, s>>>(src, nblk, dst); break;
+    case 14: quant_q6k<<<grid, block, 0, s>>>(src, nblk, dst); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace jh

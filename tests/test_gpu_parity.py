@@ -1,0 +1,396 @@
+"""GPU parity suite: libjunohip (through its C ABI) against the CPU oracle.
+
+Bars (stated per test): dequantized weights and quantizer bytes bit-exact;
+GEMV outputs within max rel-err 1e-3 with the metric
+    rel_r = |y_r - ref_r| / max(|ref_r|, 1e-3 * sum_c |w_rc x_c|)
+(fp32 accumulation, order-of-summation differences only).
+
+Inputs are seeded numpy draws, quantized with the oracle's restatement of
+LoraMerge's quantizers, so both sides see identical packed bytes.
+"""
+import os
+import subprocess
+import sys
+import threading
+
+import numpy as np
+import pytest
+
+import oracle as O
+from juno_amd import matvec as mv
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def be():
+    ctx = mv.GpuContext.shared(0)
+    info = mv.device_info(0)
+    say("device:", info)
+    assert info["arch"].startswith("gfx950")
+    return ctx.create_mat_vec()
+
+
+def weights(n, seed, outliers=False):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    if outliers:
+        idx = rng.choice(n, max(n // 100, 1), replace=False)
+        w[idx] *= 10
+    return w
+
+
+def vec(n, seed, batch=None):
+    rng = np.random.default_rng(seed)
+    shape = (n,) if batch is None else (batch, n)
+    return rng.standard_normal(shape).astype(np.float32)
+
+
+def rel_err(y, ref, deq, x):
+    """Per-row relative error with eps_r = 1e-3 * sum_c |w_rc x_c|."""
+    scale = np.abs(deq.astype(np.float64)) @ np.abs(x.astype(np.float64))
+    return np.abs(y.astype(np.float64) - ref) / np.maximum(np.abs(ref), 1e-3 * scale)
+
+
+def upload(be, qtype, raw, rows, cols):
+    return be.upload_quant(mv.QuantizedTensor("w", qtype, rows * cols, raw.tobytes()), rows, cols)
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K, O.F32])
+@pytest.mark.parametrize("outliers", [False, True])
+def test_dequant_bit_exact(be, qtype, outliers):
+    rows, cols = 96, 1024
+    say("dequant", qtype, outliers)
+    raw = O.quantize(qtype, weights(rows * cols, 21 + qtype, outliers))
+    with upload(be, qtype, raw, rows, cols) as dev:
+        got = be.dequantize(dev)
+    ref = O.dequantize(qtype, raw, rows, cols)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_random_bytes_bit_exact(be):
+    # arbitrary bytes: every scale/min/nibble pattern, subnormal and huge d values
+    rng = np.random.default_rng(5)
+    for qtype, rows, cols in [(O.Q4_K, 64, 2048), (O.Q6_K, 64, 2048), (O.Q8_0, 64, 2048)]:
+        raw = rng.integers(0, 256, O.raw_byte_count(qtype, rows * cols), dtype=np.uint8)
+        # keep d / dmin finite so the comparison is on numbers (NaN payloads aside)
+        bb, off = O.BLOCK_BYTES[qtype], {O.Q4_K: [0, 2], O.Q6_K: [208], O.Q8_0: [0]}[qtype]
+        blocks = raw.reshape(-1, bb)
+        for o in off:
+            blocks[:, o + 1] &= 0x7B  # exponent < 31
+        with upload(be, qtype, raw, rows, cols) as dev:
+            got = be.dequantize(dev)
+        ref = O.dequantize(qtype, raw, rows, cols)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), qtype
+
+
+def test_f16_scales_exhaustive_via_q8_0(be):
+    # every fp16 bit pattern as a Q8_0 scale with q = 1: dequant == f16ToF32
+    halves = np.arange(65536, dtype=np.uint32)
+    raw = np.zeros((65536, 34), dtype=np.uint8)
+    raw[:, 0] = halves & 0xFF
+    raw[:, 1] = halves >> 8
+    raw[:, 2:] = 1
+    raw = raw.reshape(-1)
+    rows, cols = 2048, 1024
+    with upload(be, O.Q8_0, raw, rows, cols) as dev:
+        got = be.dequantize(dev).reshape(65536, 32)[:, 0]
+    ref = halves.astype(np.uint16).view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_golden_q6k_block(be, golden):
+    g = golden["q6k_golden_block"]
+    blk = np.zeros(210, dtype=np.uint8)
+    blk[:128] = np.array(g["ql"]).astype(np.int8).view(np.uint8)
+    blk[128:192] = np.array(g["qh"]).astype(np.int8).view(np.uint8)
+    blk[192:208] = np.array(g["sc"]).astype(np.int8).view(np.uint8)
+    blk[208:] = [g["d_f16"] & 0xFF, g["d_f16"] >> 8]
+    with upload(be, O.Q6_K, blk, 1, 256) as dev:
+        out = be.dequantize(dev)[0]
+        y = be.sgemv_quant(dev, np.ones(256, np.float32))
+    for idx, val in g["expected"].items():
+        assert out[int(idx)] == np.float32(val)
+    assert abs(y[0] - float(out.astype(np.float64).sum())) <= 1e-3
+
+
+# ------------------------------------------------------------------ quantizer
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("outliers", [False, True])
+def test_device_quantizer_bit_exact(be, qtype, outliers):
+    import torch
+    n = 256 * 2048
+    w = weights(n, 31 + qtype, outliers)
+    w[:256] = 0.0                          # zero block
+    w[256:512] = np.float32(3e-6) * np.sign(w[256:512])   # tiny values -> subnormal fp16 d
+    w[512:768] = 1.0                       # constant block
+    say("quantize", qtype, outliers)
+    src = torch.from_numpy(w).cuda()
+    dst = torch.zeros(O.raw_byte_count(qtype, n), dtype=torch.uint8, device="cuda")
+    mv.quantize_dev(qtype, src.data_ptr(), n, dst.data_ptr())
+    torch.cuda.synchronize()
+    assert np.array_equal(dst.cpu().numpy(), O.quantize(qtype, w))
+
+
+# ------------------------------------------------------------------ GEMV
+
+SHAPES = [
+    (O.Q4_K, 5632, 2048),    # config 1: TinyLlama FFN up
+    (O.Q4_K, 2048, 2048),
+    (O.Q4_K, 256, 5632),     # nb = 22, not a multiple of 8
+    (O.Q4_K, 1, 256),        # one row, one block
+    (O.Q4_K, 37, 768),       # ragged rows, nb = 3
+    (O.Q6_K, 2048, 5632),    # TinyLlama ffn_down (4620-byte rows)
+    (O.Q6_K, 1000, 3072),    # Phi-3 sizes, odd row count
+    (O.Q6_K, 3, 256),
+    (O.Q8_0, 2304, 3072),    # Phi-3 fused QKV slice
+    (O.Q8_0, 129, 8192),
+    (O.Q8_0, 5, 32),         # one block per row
+    (O.F32, 513, 384),
+    (O.F32, 7, 3),
+]
+
+
+@pytest.mark.parametrize("qtype,rows,cols", SHAPES)
+def test_gemv_vs_oracle(be, qtype, rows, cols):
+    say("gemv", qtype, rows, cols)
+    raw = O.quantize(qtype, weights(rows * cols, rows + cols + qtype, outliers=qtype == O.Q8_0))
+    x = vec(cols, 7 + cols)
+    with upload(be, qtype, raw, rows, cols) as dev:
+        y = be.sgemv_quant(dev, x)
+    ref = O.matvec(qtype, raw, x, 0, rows, cols)
+    deq = O.dequantize(qtype, raw, rows, cols)
+    assert rel_err(y, ref.astype(np.float64), deq, x).max() <= TOL
+
+
+def test_gemv_row_ranges(be):
+    rows, cols = 3000, 2048
+    for qtype in (O.Q4_K, O.Q6_K, O.Q8_0):
+        raw = O.quantize(qtype, weights(rows * cols, 41))
+        x = vec(cols, 42)
+        deq = O.dequantize(qtype, raw, rows, cols)
+        with upload(be, qtype, raw, rows, cols) as dev:
+            for a, b in [(0, 1), (1, 2), (0, 2), (1024, 2048), (2048, 3000), (7, 1999), (2999, 3000), (5, 5)]:
+                y = be.sgemv_quant(dev, x, a, b)
+                assert y.shape == (b - a,)
+                if b > a:
+                    ref = O.matvec(qtype, raw, x, a, b, cols)
+                    assert rel_err(y, ref.astype(np.float64), deq[a:b], x).max() <= TOL, (qtype, a, b)
+
+
+def test_known_answers(be, golden):
+    g = golden["q4k_all_ff_dot_ones"]
+    blk = np.zeros(144, dtype=np.uint8)
+    blk[0:2] = [g["d_f16"] & 0xFF, g["d_f16"] >> 8]
+    blk[4] = g["sc0"]
+    blk[16:] = g["qs_fill"]
+    with upload(be, O.Q4_K, blk, 1, 256) as dev:
+        assert be.sgemv_quant(dev, np.ones(256, np.float32))[0] == g["expected_dot_ones"]
+    g = golden["q4k_fused_rows"]
+    raw = np.zeros((3, 144), dtype=np.uint8)
+    for i, r in enumerate(g["rows"]):
+        raw[i, 0:2] = [r["d_f16"] & 0xFF, r["d_f16"] >> 8]
+        raw[i, 4] = g["sc0"]
+        raw[i, 16:] = r["qs_fill"]
+    with upload(be, O.Q4_K, raw.reshape(-1), 3, 256) as dev:
+        x = np.ones(256, np.float32)
+        assert list(be.sgemv_quant(dev, x)) == g["expected_dot_ones"]
+        for a, b in g["row_ranges"]:
+            assert list(be.sgemv_quant(dev, x, a, b)) == g["expected_dot_ones"][a:b]
+
+
+def test_zero_inputs(be):
+    for qtype in (O.Q4_K, O.Q6_K, O.Q8_0):
+        rows, cols = 64, 512
+        raw = O.quantize(qtype, weights(rows * cols, 3))
+        with upload(be, qtype, raw, rows, cols) as dev:
+            assert np.all(be.sgemv_quant(dev, np.zeros(cols, np.float32)) == 0.0)
+        zraw = O.quantize(qtype, np.zeros(rows * cols, np.float32))
+        with upload(be, qtype, zraw, rows, cols) as dev:
+            assert np.all(be.sgemv_quant(dev, vec(cols, 4)) == 0.0)
+
+
+def test_x_not_mutated(be):
+    rows, cols = 128, 1024
+    raw = O.quantize(O.Q4_K, weights(rows * cols, 5))
+    x = vec(cols, 6)
+    x0 = x.copy()
+    with upload(be, O.Q4_K, raw, rows, cols) as dev:
+        be.sgemv_quant(dev, x)
+    assert np.array_equal(x, x0)
+
+
+@pytest.mark.parametrize("B", [1, 2, 3, 5, 8, 11, 16, 32])
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.Q8_0])
+def test_batched_vs_independent(be, qtype, B):
+    rows, cols = 1024, 2048
+    say("batched", qtype, B)
+    raw = O.quantize(qtype, weights(rows * cols, 50 + B))
+    X = vec(cols, 60 + B, batch=B)
+    deq = O.dequantize(qtype, raw, rows, cols)
+    with upload(be, qtype, raw, rows, cols) as dev:
+        Y = be.sgemv_batched(dev, X)
+        y1 = be.sgemv_quant(dev, X[-1])
+    assert Y.shape == (B, rows)
+    for j in range(B):
+        ref = O.matvec(qtype, raw, X[j], 0, rows, cols)
+        assert rel_err(Y[j], ref.astype(np.float64), deq, X[j]).max() <= TOL, j
+    assert rel_err(y1, Y[-1].astype(np.float64), deq, X[-1]).max() <= TOL
+
+
+def test_batched_row_range(be):
+    rows, cols, B = 700, 1024, 16
+    raw = O.quantize(O.Q4_K, weights(rows * cols, 70))
+    X = vec(cols, 71, batch=B)
+    deq = O.dequantize(O.Q4_K, raw, rows, cols)
+    with upload(be, O.Q4_K, raw, rows, cols) as dev:
+        Y = be.sgemv_batched(dev, X, 100, 333)
+    for j in range(B):
+        ref = O.matvec(O.Q4_K, raw, X[j], 100, 333, cols)
+        assert rel_err(Y[j], ref.astype(np.float64), deq[100:333], X[j]).max() <= TOL
+
+
+# ------------------------------------------------------------------ contract (MatVecBackendContractTest)
+
+def test_contract_sgemv(be, golden):
+    g = golden["contract_identity_2x3"]
+    y = be.sgemv(np.array(g["matrix"], np.float32), np.array(g["x"], np.float32), 2, 3)
+    assert np.allclose(y, g["expected"], atol=1e-6)
+    g = golden["f32_matvec_4x4"]
+    assert list(be.sgemv(np.array(g["matrix"], np.float32), np.array(g["x"], np.float32), 4, 4)) == g["expected"]
+    rng = np.random.default_rng(20)
+    for rows, cols in [(32, 32), (256, 256), (2048, 2048), (5632, 2048), (2048, 5632), (1, 512), (128, 1)]:
+        A = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+        x = (rng.standard_normal(cols) * 0.02).astype(np.float32)
+        ref = A.reshape(rows, cols).astype(np.float64) @ x.astype(np.float64)
+        assert np.abs(be.sgemv(A, x, rows, cols) - ref).max() < 1e-4  # DELTA of the contract suite
+    with pytest.raises(mv.IllegalArgumentException, match=r"rows\*cols"):
+        be.sgemv(np.zeros(10, np.float32), np.zeros(4, np.float32), 3, 4)
+    with pytest.raises(mv.IllegalArgumentException, match="cols"):
+        be.sgemv(np.zeros(12, np.float32), np.zeros(5, np.float32), 3, 4)
+
+
+def test_argument_errors(be):
+    rows, cols = 4, 256
+    raw = O.quantize(O.Q4_K, weights(rows * cols, 1))
+    with pytest.raises(mv.IllegalArgumentException, match="rawByteCount"):
+        be.upload_quant(O.Q4_K, rows, cols, raw[:-1])
+    with pytest.raises(mv.IllegalArgumentException, match="cols"):
+        be.upload_quant(O.Q4_K, 1, 300, np.zeros(144, np.uint8))
+    with pytest.raises(mv.UnsupportedOperationException):
+        be.upload_quant(10, 1, 256, np.zeros(84, np.uint8))
+    dev = upload(be, O.Q4_K, raw, rows, cols)
+    with pytest.raises(mv.IllegalArgumentException, match="cols"):
+        be.sgemv_quant(dev, np.zeros(cols + 1, np.float32))
+    with pytest.raises(mv.IllegalArgumentException, match="row range"):
+        be.sgemv_quant(dev, np.zeros(cols, np.float32), 2, 5)
+    dev.close()
+    dev.close()  # idempotent
+    with pytest.raises(mv.IllegalStateException, match="closed"):
+        be.sgemv_quant(dev, np.zeros(cols, np.float32))
+
+
+def test_device_pointer_variants(be):
+    import torch
+    rows, cols, B = 1536, 4096, 4
+    raw = O.quantize(O.Q4_K, weights(rows * cols, 80))
+    X = vec(cols, 81, batch=B)
+    deq = O.dequantize(O.Q4_K, raw, rows, cols)
+    dX = torch.from_numpy(X).cuda()
+    dY = torch.zeros((B, rows - 100), device="cuda")
+    dD = torch.zeros((rows, cols), device="cuda")
+    s = torch.cuda.Stream()
+    with upload(be, O.Q4_K, raw, rows, cols) as dev:
+        with torch.cuda.stream(s):
+            be.sgemv_dev(dev, dX.data_ptr(), dY.data_ptr(), 100, rows, stream=s.cuda_stream, batch=B)
+            be.dequantize_dev(dev, dD.data_ptr(), stream=s.cuda_stream)
+        s.synchronize()
+    Y = dY.cpu().numpy()
+    for j in range(B):
+        ref = O.matvec(O.Q4_K, raw, X[j], 100, rows, cols)
+        assert rel_err(Y[j], ref.astype(np.float64), deq[100:], X[j]).max() <= TOL
+    assert np.array_equal(dD.cpu().numpy().view(np.uint32), deq.view(np.uint32))
+
+
+def test_concurrent_threads(be):
+    # N host threads x distinct matrices, each compared to the oracle
+    rows, cols = 2048, 2048
+    mats = []
+    for i, qtype in enumerate([O.Q4_K, O.Q6_K, O.Q8_0, O.Q4_K]):
+        raw = O.quantize(qtype, weights(rows * cols, 90 + i))
+        x = vec(cols, 95 + i)
+        mats.append((qtype, raw, x, O.matvec(qtype, raw, x, 0, rows, cols), O.dequantize(qtype, raw, rows, cols)))
+    devs = [upload(be, q, raw, rows, cols) for q, raw, *_ in mats]
+    errors = []
+
+    def worker(k):
+        try:
+            q, raw, x, ref, deq = mats[k]
+            for _ in range(20):
+                y = be.sgemv_quant(devs[k], x)
+                if rel_err(y, ref.astype(np.float64), deq, x).max() > TOL:
+                    errors.append(k)
+        except Exception as e:  # pragma: no cover
+            errors.append(repr(e))
+
+    ts = [threading.Thread(target=worker, args=(k,)) for k in range(len(mats))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=60)
+    for d in devs:
+        d.close()
+    assert not errors
+
+
+def test_alloc_failure_reports_hipmalloc():
+    # LlamaTransformerHandler.java:340-357 falls back to the CPU when the
+    # upload error names hipMalloc; force it from the host in a child process.
+    code = (
+        "import numpy as np\n"
+        "from juno_amd import matvec as mv\n"
+        "be = mv.GpuContext.shared(0).create_mat_vec()\n"
+        "a = be.upload_quant(12, 1, 256, np.zeros(144, np.uint8))\n"
+        "try:\n"
+        "    be.upload_quant(12, 1, 256, np.zeros(144, np.uint8))\n"
+        "except mv.IllegalStateException as e:\n"
+        "    assert 'hipMalloc' in str(e), str(e)\n"
+        "    print('fallback-ok')\n"
+        "a.close()\n"
+    )
+    env = dict(os.environ, JUNO_HIP_FAIL_ALLOC_AFTER="1")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", code], env=env, cwd=root, capture_output=True, text=True, timeout=120)
+    assert "fallback-ok" in r.stdout, r.stdout + r.stderr
+
+
+# ------------------------------------------------------------------ full sizes, size-independent properties
+
+def test_llama8b_shapes_full_size(be):
+    """Full 8B shapes: gate/up Q4_K 14336x4096 and ffn_down Q6_K 4096x14336 vs the
+    oracle (multi-threaded), plus linearity W(a x1 + b x2) = a W x1 + b W x2."""
+    for qtype, rows, cols in [(O.Q4_K, 14336, 4096), (O.Q6_K, 4096, 14336), (O.Q4_K, 1024, 4096)]:
+        say("full", qtype, rows, cols)
+        raw = O.quantize(qtype, weights(rows * cols, 100 + rows))
+        x1, x2 = vec(cols, 101), vec(cols, 102)
+        deq = O.dequantize(qtype, raw, rows, cols)
+        with upload(be, qtype, raw, rows, cols) as dev:
+            y1 = be.sgemv_quant(dev, x1)
+            y2 = be.sgemv_quant(dev, x2)
+            y12 = be.sgemv_quant(dev, (np.float32(0.5) * x1 + np.float32(2.0) * x2).astype(np.float32))
+        ref = O.matvec(qtype, raw, x1, 0, rows, cols)
+        assert rel_err(y1, ref.astype(np.float64), deq, x1).max() <= TOL
+        lin = 0.5 * y1.astype(np.float64) + 2.0 * y2.astype(np.float64)
+        xs = np.abs(x1) * 0.5 + np.abs(x2) * 2.0
+        assert rel_err(y12, lin, deq, xs).max() <= 2 * TOL
