@@ -148,12 +148,15 @@ def dominant_kernel(torch, L, mats, stream, reps):
 def d2h_packed(torch, dev):
     """Copy a matrix's packed bytes to host memory."""
     import numpy as np
-    hbuf = np.empty(dev.nbytes(), dtype=np.uint8)
+    n = dev.nbytes()
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch already loaded
     torch.cuda.synchronize()
-    rc = torch.cuda.cudart().cudaMemcpy(hbuf.ctypes.data, dev.device_pointer(), dev.nbytes(), 2)
-    if int(rc) != 0:
-        raise RuntimeError(f"D2H copy failed: {rc}")
-    return hbuf
+    rc = hip.hipMemcpy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dev.device_pointer()),
+                       ctypes.c_size_t(n), 3)  # device to device
+    if rc != 0:
+        raise RuntimeError(f"hipMemcpy failed: rc={rc}")
+    return src.cpu().numpy()
 
 
 def cpu_baseline(torch, mats, budget_s):

@@ -170,6 +170,8 @@ int check_range(const jh_qmat *m, int row_start, int row_end) {
     return JH_OK;
 }
 
+int gemv_path();
+
 // Enqueue y = W x for B vectors (device pointers), splitting B into the
 // kernel's supported batch widths, or using the MFMA path for B >= 16.
 int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int row_start, int row_end,
@@ -193,6 +195,14 @@ int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int ro
         if (rc == hipSuccess) return JH_OK;
         if (rc != hipErrorNotSupported) return hip_fail("gemm_mfma launch", rc);
     }
+    if (B == 1 && gemv_path() != 1) {
+        a.batch = 1;
+        a.x = d_x;
+        a.y = d_y;
+        hipError_t rc = jh::launch_gemv_staged(a, s);
+        if (rc == hipSuccess) return JH_OK;
+        if (rc != hipErrorNotSupported) return hip_fail("gemv_staged launch", rc);
+    }
     int done = 0;
     while (done < B) {
         int left = B - done;
@@ -205,6 +215,16 @@ int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int ro
         done += w;
     }
     return JH_OK;
+}
+
+// JUNO_GEMV_PATH=basic forces the per-lane-block kernels of jh_gemv.hip for
+// B = 1 (A/B measurements); the default uses the staged kernels where they apply.
+int gemv_path() {
+    static const int p = [] {
+        const char *v = getenv("JUNO_GEMV_PATH");
+        return (v && strcmp(v, "basic") == 0) ? 1 : 0;
+    }();
+    return p;
 }
 
 int set_device(int dev) {

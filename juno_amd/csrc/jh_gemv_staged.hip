@@ -1,0 +1,558 @@
+// jh_gemv_staged.hip -- B = 1 fused dequant-GEMV for Q4_K, Q6_K and Q8_0 on gfx950.
+//
+// Design (measured on MI355X; each point removed a bottleneck of the simpler
+// per-lane-block kernels in jh_gemv.hip):
+//
+//  * Coalesced weight stream.  A wavefront loads the bytes of its rows as one
+//    contiguous span, 16 bytes per lane per instruction (1 KB per wave
+//    instruction), and parks them in a wave-private LDS buffer.  Lanes then
+//    read the block fields they need from LDS.  Letting each lane fetch its own
+//    block fields straight from HBM touches ~4x more cache lines per
+//    instruction and costs ~40% of the bandwidth.
+//  * Software pipeline.  The next row group's loads are issued into registers
+//    before the current group is computed from the wave's LDS buffer, so HBM
+//    latency is hidden by the dequant math of the group in hand.
+//  * Integer inner product.  x is converted once per workgroup into a 24-bit
+//    integer per element (one scale per 256 columns) held as three byte limbs,
+//    and the weights' integer quants are multiplied with v_dot4 (i8 / u8).
+//    This needs ~1.7 VALU instructions per Q4_K weight instead of ~2.8 for an
+//    fp32 convert+FMA path, which would otherwise bound the kernel below the
+//    HBM roofline.  Block scales (d, dmin, 6-bit / int8 sub-scales) are fp32.
+//  * Persistent workgroups.  x is prepared once per workgroup and kept in
+//    registers while the workgroup walks many row groups.
+//  * Wide rows (more than 16 super-blocks, or 64 Q8_0 blocks) are split into
+//    column tiles over 2 or 4 waves of a workgroup; the partial sums meet in LDS.
+//
+// Numerics: weights are used exactly; the only approximation beyond fp32
+// summation order is rounding x to 24 bits of its 256-column block maximum
+// (error <= 2^-24 * max|x| per element), the size of an fp32 rounding.
+#include "jh_device.hpp"
+#include "jh_kernels.hpp"
+
+#include <stdlib.h>
+
+namespace jh {
+namespace {
+
+// --------------------------------------------------------------------------- helpers
+
+__device__ __forceinline__ float wave_max_all(float v) {
+    int x = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true)));
+    x = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true)));
+    x = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, true)));
+    x = __builtin_bit_cast(int, v);
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true)));
+    x = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Sum over the wavefront with DPP only; the total is valid in lane 63.
+__device__ __forceinline__ float wave_sum_to63(float v) {
+    int x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true));  // quad_perm 1,0,3,2
+    x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true));  // quad_perm 2,3,0,1
+    x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, true));  // row_ror:4
+    x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true));  // row_ror:8
+    x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false));  // row_bcast:15
+    x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false));  // row_bcast:31
+    return v;
+}
+
+__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+__device__ __forceinline__ int udot4(uint32_t a, uint32_t b, int c) {
+    return (int)__builtin_amdgcn_udot4(a, b, (uint32_t)c, false);
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// 4 bytes at a 2-byte-aligned LDS address given as (dword pointer, byte shift).
+__device__ __forceinline__ uint32_t lds_word(const uint32_t *w, uint32_t sh, int k) {
+    return __builtin_amdgcn_alignbyte(w[k + 1], w[k], sh);
+}
+
+// --------------------------------------------------------------------------- x preparation
+//
+// Every x element becomes a 24-bit integer xi = rint(x / a) with one scale
+// a = max|x| / (2^23 - 1) per 256 columns, split into three byte limbs
+//   xi = 65536 * hi + 256 * mid + lo,   hi signed, mid and lo unsigned,
+// so that sum(q * x) = a * (65536 * sum(q*hi) + 256 * sum(q*mid) + sum(q*lo))
+// with three v_dot4 products per 4 quants and exact integer sums.  The
+// resolution is 2^-23 of the block maximum (about fp32's), so the integer
+// path adds no error of consequence to the fp32 accumulation.
+//
+// LDS image: hi | mid | lo  [cols_pad] int8 each, scale[nblk] f32 (= a),
+// xs16[cols_pad/16] f32 (exact fp32 sums of 16 x), smid32 / slo32
+// [cols_pad/32] i32 (sums of the mid / lo limbs over 32 columns, for the
+// signed Q8_0 quants).  cols_pad = 256 * nblk; columns >= cols read as 0.
+
+struct XImage {
+    int cols, nblk;
+    uint8_t *base;
+    __device__ uint32_t *hi() const { return reinterpret_cast<uint32_t *>(base); }
+    __device__ uint32_t *mid() const { return reinterpret_cast<uint32_t *>(base + 256 * nblk); }
+    __device__ uint32_t *lo() const { return reinterpret_cast<uint32_t *>(base + 512 * nblk); }
+    __device__ float *scale() const { return reinterpret_cast<float *>(base + 768 * nblk); }
+    __device__ float *xs16() const { return scale() + nblk; }
+    __device__ int *smid32() const { return reinterpret_cast<int *>(xs16() + 16 * nblk); }
+    __device__ int *slo32() const { return smid32() + 8 * nblk; }
+    static __host__ __device__ size_t bytes(int nblk) { return (size_t)nblk * (768 + 4 + 64 + 32 + 32); }
+};
+
+// cols is a multiple of 32: a float4 is either wholly inside or wholly past
+// the end.  The load is clamped in range; x_quant_block zeroes the float4s
+// that lie past the end (at use, so the load is not waited for here).
+__device__ __forceinline__ float4 x_load4(const float *X, int cols, int c) {
+    return *reinterpret_cast<const float4 *>(X + min(c, cols - 4));
+}
+
+__device__ __forceinline__ void x_quant_block(const XImage &im, int b, float4 v) {
+    const int lane = threadIdx.x & 63;
+    if (b * 256 + lane * 4 >= im.cols) v = make_float4(0.f, 0.f, 0.f, 0.f);
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    m = wave_max_all(m);
+    constexpr float kMaxInt = 8388607.f;  // 2^23 - 1
+    const float a = m * (1.f / kMaxInt);
+    const float inv = m > 0.f ? kMaxInt / m : 0.f;
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    uint32_t ph = 0, pm = 0, pl = 0;
+    int sm = 0, sl = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int xi = max(-8388607, min(8388607, (int)rintf(e[j] * inv)));
+        const uint32_t u = (uint32_t)xi;
+        ph |= ((u >> 16) & 0xFFu) << (8 * j);
+        pm |= ((u >> 8) & 0xFFu) << (8 * j);
+        pl |= (u & 0xFFu) << (8 * j);
+        sm += (int)((u >> 8) & 0xFFu);
+        sl += (int)(u & 0xFFu);
+    }
+    im.hi()[b * 64 + lane] = ph;
+    im.mid()[b * 64 + lane] = pm;
+    im.lo()[b * 64 + lane] = pl;
+    float s = (v.x + v.y) + (v.z + v.w);
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    if ((lane & 3) == 0) im.xs16()[b * 16 + (lane >> 2)] = s;
+    sm += __shfl_xor(sm, 1);
+    sl += __shfl_xor(sl, 1);
+    sm += __shfl_xor(sm, 2);
+    sl += __shfl_xor(sl, 2);
+    sm += __shfl_xor(sm, 4);
+    sl += __shfl_xor(sl, 4);
+    if ((lane & 7) == 0) {
+        im.smid32()[b * 8 + (lane >> 3)] = sm;
+        im.slo32()[b * 8 + (lane >> 3)] = sl;
+    }
+    if (lane == 0) im.scale()[b] = a;
+}
+
+// 65536*h + 256*m + l of three dot-product partial sums, in fp32.
+__device__ __forceinline__ float limbs(int h, int m, int l) {
+    return fmaf((float)h, 65536.f, fmaf((float)m, 256.f, (float)l));
+}
+
+// --------------------------------------------------------------------------- formats
+
+// Per-format constants: block quant count, block bytes, lanes per block, max
+// blocks per wave tile, max 16-byte chunks of one row tile in LDS.
+template <int T> struct Fmt;
+template <> struct Fmt<12> { static constexpr int QK = 256, BB = 144, LPB = 4, TBMAX = 16, CH = 145; };
+template <> struct Fmt<14> { static constexpr int QK = 256, BB = 210, LPB = 4, TBMAX = 16, CH = 212; };
+template <> struct Fmt<8> { static constexpr int QK = 32, BB = 34, LPB = 1, TBMAX = 64, CH = 138; };
+
+// x registers a lane keeps for its block slot: N dwords per limb.
+template <int N> struct XLimbs {
+    uint32_t h[N], m[N], l[N];
+    __device__ void load_run(const XImage &im, int dw, int at, int n) {  // n dwords from dword index dw
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (k >= n / 4) break;
+            const uint4 t = *reinterpret_cast<const uint4 *>(im.hi() + dw + 4 * k);
+            h[at + 4 * k] = t.x; h[at + 4 * k + 1] = t.y; h[at + 4 * k + 2] = t.z; h[at + 4 * k + 3] = t.w;
+            const uint4 u = *reinterpret_cast<const uint4 *>(im.mid() + dw + 4 * k);
+            m[at + 4 * k] = u.x; m[at + 4 * k + 1] = u.y; m[at + 4 * k + 2] = u.z; m[at + 4 * k + 3] = u.w;
+            const uint4 w = *reinterpret_cast<const uint4 *>(im.lo() + dw + 4 * k);
+            l[at + 4 * k] = w.x; l[at + 4 * k + 1] = w.y; l[at + 4 * k + 2] = w.z; l[at + 4 * k + 3] = w.w;
+        }
+    }
+};
+
+template <int T> struct XRegs;
+
+template <> struct XRegs<12> : XLimbs<16> {  // 64 columns: sub-blocks 2g ([0..7]) and 2g+1 ([8..15])
+    float a, xs0, xs1;
+    __device__ void load(const XImage &im, int b, int g, bool act) {
+        load_run(im, (b * 256 + 64 * g) / 4, 0, 16);
+        const float4 s = *reinterpret_cast<const float4 *>(im.xs16() + b * 16 + 4 * g);
+        a = act ? im.scale()[b] : 0.f;
+        xs0 = act ? s.x + s.y : 0.f;
+        xs1 = act ? s.z + s.w : 0.f;
+    }
+};
+
+template <> struct XRegs<14> : XLimbs<16> {  // runs k = 0..3 of 16 columns: b*256 + hh*128 + 32k + l0
+    float a, m32[4];
+    __device__ void load(const XImage &im, int b, int g, bool act) {
+        const int hh = g >> 1, l0 = 16 * (g & 1);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int c = b * 256 + hh * 128 + 32 * k + l0;
+            load_run(im, c / 4, 4 * k, 4);
+            m32[k] = act ? -32.f * im.xs16()[c / 16] : 0.f;
+        }
+        a = act ? im.scale()[b] : 0.f;
+    }
+};
+
+template <> struct XRegs<8> : XLimbs<8> {  // 32 columns of block b
+    float a;
+    int sm, sl;  // limb sums, for the +128 bias of the signed quants
+    __device__ void load(const XImage &im, int b, int, bool act) {
+        load_run(im, b * 8, 0, 8);
+        a = act ? im.scale()[b / 8] : 0.f;
+        sm = im.smid32()[b];
+        sl = im.slo32()[b];
+    }
+};
+
+// Dot product of one block slot of one row (block bytes at LDS byte address p).
+// Q4_K (LlamaTransformerHandler.java:1428-1468): sum over sub-blocks 2g, 2g+1 of
+//   d*ls*sum(q*x) - dmin*lm*sum(x).
+__device__ __forceinline__ float block_dot(const XRegs<12> &x, const uint8_t *p, int g) {
+    const uint4 hd = *reinterpret_cast<const uint4 *>(p);
+    const uint4 qa = *reinterpret_cast<const uint4 *>(p + 16 + 32 * g);
+    const uint4 qb = *reinterpret_cast<const uint4 *>(p + 32 + 32 * g);
+    const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+        h0 = sdot4(lo, x.h[k], h0);
+        m0 = udot4(lo, x.m[k], m0);
+        l0 = udot4(lo, x.l[k], l0);
+        h1 = sdot4(hi, x.h[8 + k], h1);
+        m1 = udot4(hi, x.m[8 + k], m1);
+        l1 = udot4(hi, x.l[8 + k], l1);
+    }
+    // 6-bit scale / min of sub-blocks j = 2g, 2g+1 (q4kScaleRaw / q4kMinRaw,
+    // LlamaTransformerHandler.java:1471-1482), branch-free: for g >= 2 the low
+    // 4 bits come from bytes 8..11 and the top 2 bits from bytes 0..7.
+    const bool hiG = g >= 2;
+    const int jj = (2 * g) & 3, wl = hiG ? 4 : 6, wh = hiG ? 2 : 0, mo = hiG ? 4 : 0;
+    const uint32_t wls = hiG ? hd.w : hd.y, wlm = hiG ? hd.w : hd.z;
+    const int ls0 = (int)(__builtin_amdgcn_ubfe(wls, 8 * jj, wl) | (__builtin_amdgcn_ubfe(hd.y, 8 * jj + 6, wh) << 4));
+    const int ls1 = (int)(__builtin_amdgcn_ubfe(wls, 8 * jj + 8, wl) | (__builtin_amdgcn_ubfe(hd.y, 8 * jj + 14, wh) << 4));
+    const int lm0 = (int)(__builtin_amdgcn_ubfe(wlm, 8 * jj + mo, wl) | (__builtin_amdgcn_ubfe(hd.z, 8 * jj + 6, wh) << 4));
+    const int lm1 = (int)(__builtin_amdgcn_ubfe(wlm, 8 * jj + 8 + mo, wl) | (__builtin_amdgcn_ubfe(hd.z, 8 * jj + 14, wh) << 4));
+    const float t = fmaf((float)ls1, limbs(h1, m1, l1), (float)ls0 * limbs(h0, m0, l0));
+    const float mn = fmaf((float)lm1, x.xs1, (float)lm0 * x.xs0);
+    const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
+    return fmaf(d * x.a, t, -dmin * mn);
+}
+
+// Q6_K (LlamaTransformerHandler.java:1587-1638): lane g covers half hh = g/2 and
+// l in [l0, l0+16), l0 = 16*(g&1), for the four quads k (elements l + 32k).
+// q = u - 32 with u = (ql nibble) | (2 qh bits) << 4; scale d * sc[hh*8 + (g&1) + 2k].
+__device__ __forceinline__ float block_dot(const XRegs<14> &x, const uint8_t *p, int g) {
+    const int hh = g >> 1, l0 = 16 * (g & 1);
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(p);
+    const uint32_t sh = (uint32_t)(pa & 3u);
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(p - sh);
+    const uint32_t *wa = w + (hh * 64 + l0) / 4;
+    const uint32_t *wb = w + (hh * 64 + 32 + l0) / 4;
+    const uint32_t *wq = w + (128 + hh * 32 + l0) / 4;
+    const uint32_t *ws = w + (192 + hh * 8) / 4;
+    const uint32_t *wd = w + 208 / 4;
+    int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t a = lds_word(wa, sh, k), b = lds_word(wb, sh, k), e = lds_word(wq, sh, k);
+        const uint32_t u[4] = {(a & 0x0F0F0F0Fu) | ((e << 4) & 0x30303030u),
+                               (b & 0x0F0F0F0Fu) | ((e << 2) & 0x30303030u),
+                               ((a >> 4) & 0x0F0F0F0Fu) | (e & 0x30303030u),
+                               ((b >> 4) & 0x0F0F0F0Fu) | ((e >> 2) & 0x30303030u)};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            ah[j] = sdot4(u[j], x.h[4 * j + k], ah[j]);
+            am[j] = udot4(u[j], x.m[4 * j + k], am[j]);
+            al[j] = udot4(u[j], x.l[4 * j + k], al[j]);
+        }
+    }
+    const uint32_t s0 = lds_word(ws, sh, 0), s1 = lds_word(ws, sh, 1);
+    const uint32_t dword = lds_word(wd, sh, 0);
+    const int is = g & 1;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int idx = is + 2 * j;  // 0..7 within this half's 8 scale bytes
+        const int sc = (int)(int8_t)byte_of(idx < 4 ? s0 : s1, idx & 3);
+        acc = fmaf((float)sc, fmaf(x.a, limbs(ah[j], am[j], al[j]), x.m32[j]), acc);
+    }
+    return half_bits_to_float(dword) * acc;
+}
+
+// Q8_0 (LlamaTransformerHandler.java:1486-1508): one lane per 34-byte block.
+// The signed quants enter the unsigned mid / lo products as q + 128.
+__device__ __forceinline__ float block_dot(const XRegs<8> &x, const uint8_t *p, int) {
+    const uintptr_t pa = reinterpret_cast<uintptr_t>(p);
+    const uint32_t sh = (uint32_t)(pa & 3u);
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(p - sh);
+    const float d = half_bits_to_float(lds_word(w, sh, 0));
+    int h = 0, m = 0, l = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        // quants start 2 bytes into the block
+        const uint32_t q = __builtin_amdgcn_alignbyte(w[k + 1 + (sh >> 1)], w[k + (sh >> 1)], (sh + 2) & 3);
+        const uint32_t qb = q ^ 0x80808080u;
+        h = sdot4(q, x.h[k], h);
+        m = udot4(qb, x.m[k], m);
+        l = udot4(qb, x.l[k], l);
+    }
+    m -= 128 * x.sm;
+    l -= 128 * x.sl;
+    return d * x.a * limbs(h, m, l);
+}
+
+// --------------------------------------------------------------------------- kernel
+
+struct StagedArgs {
+    const uint8_t *w;  // matrix base (row 0), 256-byte aligned (hipMalloc)
+    int row0;          // first row to compute
+    size_t pitch;
+    int nb, nrows, cols;
+    int gw;   // waves per row group (column tiles): 1, 2 or 4
+    int tb;   // blocks per tile
+    const float *x;
+    float *y;
+};
+
+template <int T, int R>
+__global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
+    using F = Fmt<T>;
+    constexpr int K = (F::CH + 63) / 64;  // 16-byte loads per lane per row
+    extern __shared__ __align__(16) uint8_t lds[];
+    // wave-uniform values live in SGPRs: derive them from a readfirstlane'd wave id
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int nb = args.nb, nrows = args.nrows, gw = args.gw, tb = args.tb;
+    const size_t pitch = args.pitch;
+    const int nblk = (args.cols + 255) / 256;
+    XImage im{args.cols, nblk, lds};
+    uint4 *stage = reinterpret_cast<uint4 *>(lds + ((XImage::bytes(nblk) + 15) & ~size_t(15)));
+    uint4 *buf0 = stage + wave * R * F::CH;
+    float *part = reinterpret_cast<float *>(stage + 4 * R * F::CH);  // [2][4][R]
+
+    const int slots = 4 / gw;  // row groups processed side by side by one workgroup
+    const int tile = wave % gw, slot = wave / gw;
+    const int ngroups = (nrows + R - 1) / R;
+    const int gstride = gridDim.x * slots;
+    int grp = blockIdx.x * slots + slot;
+
+    const int blk = lane / F::LPB, sub = lane % F::LPB;
+    const int b0 = tile * tb;                        // first block of this wave's tile
+    const int ntile = min(tb, nb - b0);              // blocks in this tile
+    const bool act = blk < ntile;
+    const int b = b0 + (act ? blk : 0);
+    const size_t tile_off = (size_t)b0 * F::BB;
+    const int tile_bytes = ntile * F::BB;
+    const int nch = (int)((15 + tile_bytes + 15) >> 4);  // chunks to cover any 2-byte-aligned start
+    int ld_off[K];                                        // per-lane chunk offsets (clamped)
+#pragma unroll
+    for (int k = 0; k < K; k++) ld_off[k] = 16 * min(lane + 64 * k, nch - 1);
+    const int lane_blk = (act ? blk : 0) * F::BB;
+
+    // 1. first x loads (before any weight load, so waiting for x does not
+    //    wait for the weight stream); up to 4 blocks of 256 per wave
+    float4 xv[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) xv[k] = x_load4(args.x, args.cols, (wave + 4 * k) * 256 + lane * 4);
+    asm volatile("" ::: "memory");
+
+    // 2. weight loads.  Byte offsets are relative to args.w, which is 256-byte
+    //    aligned, so a span's alignment follows from its offset alone.
+    uint4 v[R][K];
+    size_t start[R];  // byte offset of each row tile of the group in flight
+    auto issue = [&](int g) {
+        const int r0 = min(g, ngroups - 1) * R;
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            start[i] = (size_t)(args.row0 + min(r0 + i, nrows - 1)) * pitch + tile_off;
+            const uint8_t *base = args.w + (start[i] & ~size_t(15));
+#pragma unroll
+            for (int k = 0; k < K; k++) v[i][k] = load_stream16(base + ld_off[k]);
+        }
+    };
+    auto park = [&](uint4 *dst) {
+#pragma unroll
+        for (int i = 0; i < R; i++)
+#pragma unroll
+            for (int k = 0; k < K; k++)
+                if (lane + 64 * k < F::CH) dst[i * F::CH + lane + 64 * k] = v[i][k];
+    };
+    issue(grp);
+    asm volatile("" ::: "memory");
+
+    // 3. quantize x into LDS (blocks beyond the first 4 per wave load now)
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (wave + 4 * k < nblk) x_quant_block(im, wave + 4 * k, xv[k]);
+    for (int bx = wave + 16; bx < nblk; bx += 4) x_quant_block(im, bx, x_load4(args.x, args.cols, bx * 256 + lane * 4));
+    __syncthreads();
+    XRegs<T> xr;
+    xr.load(im, b, sub, act);
+
+    // 4. pipelined walk over row groups
+    park(buf0);
+    wave_lds_sync();
+    int it = 0;
+    while (true) {
+        size_t cstart[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) cstart[i] = start[i];
+        const int next = grp + gstride;
+        issue(next);
+        const int r0 = grp * R;
+        const uint8_t *cb = reinterpret_cast<const uint8_t *>(buf0);
+        float s[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const uint8_t *row = cb + i * F::CH * 16 + (int)(cstart[i] & 15);
+            const float d = block_dot(xr, row + lane_blk, sub);
+            s[i] = wave_sum_to63(act ? d : 0.f);
+        }
+        if (gw == 1) {
+            if (lane == 63)
+#pragma unroll
+                for (int i = 0; i < R; i++)
+                    if (r0 + i < nrows) args.y[r0 + i] = s[i];
+            if (next >= ngroups) break;
+        } else {
+            float *pp = part + (it & 1) * 4 * R;
+            if (lane == 63)
+#pragma unroll
+                for (int i = 0; i < R; i++) pp[wave * R + i] = s[i];
+            __syncthreads();
+            if (tile == 0 && lane == 63 && grp < ngroups)
+#pragma unroll
+                for (int i = 0; i < R; i++) {
+                    float t = 0.f;
+                    for (int q = 0; q < gw; q++) t += pp[(slot * gw + q) * R + i];
+                    if (r0 + i < nrows) args.y[r0 + i] = t;
+                }
+            // every wave of the workgroup iterates while slot 0 has work
+            if (next - slot >= ngroups) break;
+        }
+        // the group just computed is done with the buffer: park the next one there
+        wave_lds_sync();
+        park(buf0);
+        wave_lds_sync();
+        grp = next;
+        it++;
+    }
+}
+
+template <int T, int R>
+hipError_t launch_staged_t(const GemvArgs &a, int nb, hipStream_t s) {
+    using F = Fmt<T>;
+    StagedArgs sa;
+    sa.pitch = a.pitch;
+    sa.w = a.w;
+    sa.row0 = a.row_start;
+    sa.nb = nb;
+    sa.nrows = a.row_end - a.row_start;
+    sa.cols = a.cols;
+    sa.gw = nb <= F::TBMAX ? 1 : nb <= 2 * F::TBMAX ? 2 : 4;
+    sa.tb = (nb + sa.gw - 1) / sa.gw;
+    sa.x = a.x;
+    sa.y = a.y;
+    const int nblk = (a.cols + 255) / 256;
+    const size_t lds = ((XImage::bytes(nblk) + 15) & ~size_t(15)) + (size_t)4 * R * F::CH * 16 + 2 * 4 * R * 4;
+    const int slots = 4 / sa.gw;
+    const int ngroups = (sa.nrows + R - 1) / R;
+    // persistent grid: as many workgroups as fit at once, capped by the work
+    int per_cu = (int)(160 * 1024 / lds);
+    per_cu = per_cu < 1 ? 1 : (per_cu > 3 ? 3 : per_cu);
+    int wgs = 256 * per_cu;
+    const int need = (ngroups + slots - 1) / slots;
+    if (wgs > need) wgs = need;
+    static bool attr_set = [] {
+        // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950)
+        return hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_staged<T, R>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    }();
+    (void)attr_set;
+    gemv_staged<T, R><<<wgs, 256, lds, s>>>(sa);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool staged_supported(int type, int cols) {
+    switch (type) {
+    case 12: return cols % 256 == 0 && cols / 256 <= 4 * Fmt<12>::TBMAX;
+    case 14: return cols % 256 == 0 && cols / 256 <= 4 * Fmt<14>::TBMAX;
+    case 8: return cols % 32 == 0 && cols / 32 <= 4 * Fmt<8>::TBMAX;
+    default: return false;
+    }
+}
+
+// Rows per group; JUNO_STAGED_R (1, 2 or 4) overrides the default for tuning runs.
+static int staged_rows(int def) {
+    static const int r = [] {
+        const char *v = getenv("JUNO_STAGED_R");
+        const int x = v ? atoi(v) : 0;
+        return (x == 1 || x == 2 || x == 4) ? x : 0;
+    }();
+    return r ? r : def;
+}
+
+template <int T>
+static hipError_t launch_staged_r(const GemvArgs &a, int nb, int R, hipStream_t s) {
+    switch (R) {
+    case 1: return launch_staged_t<T, 1>(a, nb, s);
+    case 2: return launch_staged_t<T, 2>(a, nb, s);
+    default: return launch_staged_t<T, 4>(a, nb, s);
+    }
+}
+
+// The staged kernel pays a fixed prologue (x conversion, one barrier) of a
+// few microseconds; below ~28 MB of packed weights the one-shot kernels of
+// jh_gemv.hip finish first (measured on MI355X at Llama-3-8B / Phi-3 shapes).
+constexpr size_t kStagedMinBytes = 28u << 20;
+
+hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s) {
+    if (a.batch != 1 || !staged_supported(a.type, a.cols)) return hipErrorNotSupported;
+    if ((size_t)(a.row_end - a.row_start) * a.pitch < kStagedMinBytes && !getenv("JUNO_STAGED_R"))
+        return hipErrorNotSupported;
+    switch (a.type) {
+    case 12: return launch_staged_r<12>(a, a.cols / 256, staged_rows(2), s);
+    case 14: return launch_staged_r<14>(a, a.cols / 256, staged_rows(2), s);
+    case 8: return launch_staged_r<8>(a, a.cols / 32, staged_rows(2), s);
+    default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace jh

@@ -27,6 +27,11 @@ struct GemvArgs {
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
 
+// B = 1 coalesced, pipelined, int8-x kernel (jh_gemv_staged.hip); returns
+// hipErrorNotSupported for shapes it does not cover.
+bool staged_supported(int type, int cols);
+hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s);
+
 // Batched decode through the LDS-dequant + fp16 MFMA path (B >= 16).
 // Returns hipErrorNotSupported for types without an MFMA kernel.
 hipError_t launch_gemm_mfma(const GemvArgs &a, hipStream_t s);
