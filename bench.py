@@ -10,13 +10,15 @@ weights per token).  Weights are random N(0, 0.02) fp32 drawn on the device and
 quantized on the device with LoraMerge's Q4_K / Q6_K quantizers; activations are
 N(0, 1) fp32.  All inputs are resident in HBM before timing starts.
 
-A "step" is one decode token's 225 GEMVs, captured once into a HIP graph and
-replayed.  value = algorithmic bytes per step / step time (GB/s), where
+A "step" is one decode token's 225 GEMVs, issued as a decode step can issue
+them (independent GEMVs on one input share a launch: [q,k,v], [gate,up]),
+captured once into a HIP graph and replayed.  value = algorithmic bytes per step / step time (GB/s), where
 algorithmic bytes = packed weight bytes + 4*(cols + rows) per GEMV.
 
 Extra measurements in the same JSON line:
-  roofline      the dominant kernel (Q4_K gate/up GEMV 14336x4096), timed with
-                HIP events on its own stream over all 64 gate/up matrices
+  roofline      the dominant kernel (the grouped Q4_K [gate, up] GEMV, one launch
+                over 2 x 14336x4096), timed with HIP events on its stream over
+                all 32 layers' launches
   cpu_baseline  the CPU oracle (C restatement of Juno's Java matVecQ4Kraw /
                 matVecQ6Kraw, one task per row on a thread pool) on one layer's
                 GEMVs, on the host cores of this machine
@@ -79,21 +81,58 @@ def build_model(torch, be, seed=0):
     return mats
 
 
-def make_step(torch, L, mats, B, stream):
-    """Buffers and a launcher for one decode step's GEMVs at batch B."""
+def make_step(torch, L, mats, B, stream, grouped=True):
+    """Buffers and a launcher for one decode step's GEMVs at batch B.
+
+    B = 1 issues the GEMVs the way a decode step can: per layer one grouped
+    launch for [q, k, v] (same input), [o], one for [gate, up] (same input),
+    [down]; then the lm_head.  Each stage has its own input vector, as in a
+    real step (attention-norm output, attention output, FFN-norm output,
+    SwiGLU product).  B > 1 calls the batched entry point per matrix."""
     g = torch.Generator(device="cuda")
     g.manual_seed(1)
-    xs = {HIDDEN: torch.randn(B, HIDDEN, generator=g, device="cuda"),
-          FFN: torch.randn(B, FFN, generator=g, device="cuda")}
-    ys = {r: torch.empty(B, r, device="cuda") for r in {m[1] for m in mats}}
+    x_attn = torch.randn(B, HIDDEN, generator=g, device="cuda")
+    x_o = torch.randn(B, HIDDEN, generator=g, device="cuda")
+    x_ffn = torch.randn(B, HIDDEN, generator=g, device="cuda")
+    x_down = torch.randn(B, FFN, generator=g, device="cuda")
+    x_head = torch.randn(B, HIDDEN, generator=g, device="cuda")
+    src = {"attn_q": x_attn, "attn_k": x_attn, "attn_v": x_attn, "attn_output": x_o,
+           "ffn_gate": x_ffn, "ffn_up": x_ffn, "ffn_down": x_down, "output": x_head}
+    ys = {m[0]: torch.empty(B, m[1], device="cuda") for m in mats}
+    by_name = {m[0]: m for m in mats}
+    stages = []
+    for layer in range(LAYERS):
+        for names in (["attn_q", "attn_k", "attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"], ["ffn_down"]):
+            stages.append([f"blk.{layer}.{n}" for n in names])
+    stages.append(["output"])
+    if not grouped or B != 1:
+        stages = [[m[0]] for m in mats]
+
+    def xin(name):
+        return src[name.split(".")[-1]]
+
+    packed = []
+    for st in stages:
+        n = len(st)
+        hs = (ctypes.c_void_p * n)(*[by_name[nm][4].handle for nm in st])
+        xp = (ctypes.c_void_p * n)(*[xin(nm).data_ptr() for nm in st])
+        yp = (ctypes.c_void_p * n)(*[ys[nm].data_ptr() for nm in st])
+        packed.append((st, n, hs, xp, yp))
+
+    keep = (src, ys)  # the kernels write through raw pointers: keep the tensors alive
 
     def launch():
+        assert keep
         s = ctypes.c_void_p(stream.cuda_stream)
-        for _, rows, cols, _, dev in mats:
-            rc = L.jh_qmatvec_batched_dev(dev.handle, xs[cols].data_ptr(), B, ys[rows].data_ptr(), 0, rows, s)
+        for st, n, hs, xp, yp in packed:
+            if B == 1 and grouped:
+                rc = L.jh_qmatvec_group_dev(n, hs, xp, yp, s)
+            else:
+                _, rows, cols, _, dev = by_name[st[0]]
+                rc = L.jh_qmatvec_batched_dev(dev.handle, xp[0], B, yp[0], 0, rows, s)
             if rc:
                 raise RuntimeError(L.jh_last_error().decode())
-    return launch, xs, ys
+    return launch, len(packed)
 
 
 def time_graph(torch, launch, stream, steps, warmup):
@@ -120,19 +159,27 @@ def time_graph(torch, launch, stream, steps, warmup):
 
 
 def dominant_kernel(torch, L, mats, stream, reps):
-    """Average launch duration of the Q4_K gate/up GEMV (14336x4096, B=1),
-    HIP events on the launch stream, rotating over the 64 distinct matrices."""
-    sel = [m for m in mats if m[0].endswith(("ffn_gate", "ffn_up"))]
+    """Average launch duration of the dominant kernel: the grouped Q4_K [gate, up]
+    GEMV of a layer (2 x 14336x4096, one staged launch, B=1).  HIP events on the
+    launch stream around graph replays of all 32 layers' launches, so every
+    launch streams matrices no other launch in the replay touches."""
+    pairs = [([m for m in mats if m[0] == f"blk.{l}.ffn_gate"][0], [m for m in mats if m[0] == f"blk.{l}.ffn_up"][0])
+             for l in range(LAYERS)]
     x = torch.randn(HIDDEN, device="cuda")
-    y = torch.empty(FFN, device="cuda")
+    ys = [torch.empty(FFN, device="cuda") for _ in range(2)]
     s = ctypes.c_void_p(stream.cuda_stream)
+    args = []
+    for ga, ua in pairs:
+        hs = (ctypes.c_void_p * 2)(ga[4].handle, ua[4].handle)
+        xp = (ctypes.c_void_p * 2)(x.data_ptr(), x.data_ptr())
+        yp = (ctypes.c_void_p * 2)(ys[0].data_ptr(), ys[1].data_ptr())
+        args.append((hs, xp, yp))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    # one graph of the 64 launches, replayed: no host launch gaps inside the timed region
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         with torch.cuda.graph(g, stream=stream):
-            for _, rows, _, _, dev in sel:
-                L.jh_qmatvec_batched_dev(dev.handle, x.data_ptr(), 1, y.data_ptr(), 0, rows, s)
+            for hs, xp, yp in args:
+                L.jh_qmatvec_group_dev(2, hs, xp, yp, s)
         g.replay()
         stream.synchronize()
         e0.record(stream)
@@ -140,9 +187,11 @@ def dominant_kernel(torch, L, mats, stream, reps):
             g.replay()
         e1.record(stream)
         stream.synchronize()
-    avg_ms = e0.elapsed_time(e1) / (reps * len(sel))
-    per_launch = algo_bytes(FFN, HIDDEN, Q4_K)
-    return avg_ms, per_launch, sel
+    avg_ms = e0.elapsed_time(e1) / (reps * len(args))
+    per_launch = 2 * packed_bytes(FFN, HIDDEN, Q4_K) + 4 * (HIDDEN + 2 * FFN)
+    del g  # the graph goes before the buffers it writes
+    torch.cuda.synchronize()
+    return avg_ms, per_launch, pairs
 
 
 def d2h_packed(torch, dev):
@@ -241,19 +290,20 @@ def main():
         f"{time.perf_counter() - t0:.1f} s")
     stream = torch.cuda.Stream()
 
-    launch, _, _ = make_step(torch, L, mats, 1, stream)
+    launch, nlaunch = make_step(torch, L, mats, 1, stream)
     ms, wall_ms = time_graph(torch, launch, stream, args.steps, args.warmup)
     sb = step_bytes(1)
     gbs = sb / (ms * 1e-3) / 1e9
-    log(f"B=1 step: {ms:.4f} ms (wall {wall_ms:.4f} ms)  {gbs:.1f} GB/s  {1e3 / ms:.1f} tok/s")
+    log(f"B=1 step: {ms:.4f} ms (wall {wall_ms:.4f} ms, {nlaunch} grouped launches)  {gbs:.1f} GB/s  "
+        f"{1e3 / ms:.1f} tok/s")
 
     avg_ms, per_launch, _ = dominant_kernel(torch, L, mats, stream, reps=max(args.steps // 5, 4))
     ach = per_launch / (avg_ms * 1e-3) / 1e9
-    log(f"gate/up Q4_K GEMV: {avg_ms * 1e3:.2f} us/launch  {ach:.1f} GB/s")
+    log(f"gate+up Q4_K grouped GEMV: {avg_ms * 1e3:.2f} us/launch  {ach:.1f} GB/s")
 
     batched = None
     if not args.no_batched:
-        launch32, _, _ = make_step(torch, L, mats, 32, stream)
+        launch32, _ = make_step(torch, L, mats, 32, stream)
         ms32, _ = time_graph(torch, launch32, stream, max(args.steps // 5, 3), 2)
         sb32 = step_bytes(32)
         batched = {"B": 32, "ms_per_step": round(ms32, 4), "tok_s": round(32 * 1e3 / ms32, 1),
@@ -282,13 +332,15 @@ def main():
         "data": "synthetic: N(0,0.02) weights quantized on device with LoraMerge Q4_K/Q6_K; N(0,1) activations",
         "config": {"workload": "llama3-8b-q4_k_m-decode-gemvs-b1", "hidden": HIDDEN, "ffn": FFN,
                    "kv_dim": KV, "vocab": VOCAB, "layers": LAYERS, "batch": 1,
-                   "gemvs_per_step": len(mats), "q6k_rule": "attn_v, ffn_down, output in every layer",
+                   "gemvs_per_step": len(mats), "launches_per_step": nlaunch,
+                   "q6k_rule": "attn_v, ffn_down, output in every layer",
                    "algorithmic_bytes_per_step": sb},
         "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
         "tok_s": round(1e3 / ms, 1),
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "gemv_q4k 14336x4096 B=1", "avg_launch_us": round(avg_ms * 1e3, 3),
+                     "kernel": "gemv_staged<Q4_K> [gate, up] 2x14336x4096 B=1 (one launch)",
+                     "avg_launch_us": round(avg_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": per_launch},
         "cpu_baseline": cpu,
         "batched": batched,

@@ -133,6 +133,16 @@ int jh_qmatvec_batched_dev(const jh_qmat *m, const float *d_X, int B, float *d_Y
                            int row_end, void *stream);
 int jh_qmat_dequant_dev(const jh_qmat *m, float *d_out, void *stream);
 
+/* n <= 8 independent GEMVs, y_i = W_i x_i over all rows of W_i, B = 1, device
+ * pointers, enqueued on one stream in as few kernel launches as possible:
+ * large matrices of one format that share an x (gate and up) go through one
+ * staged launch, all other matrices through one one-shot launch.  Equal to n
+ * jh_qmatvec_dev calls.  The handlers issue such independent matVecs back to
+ * back on one input (Q, K, V and gate, up: LlamaTransformerHandler.java:751-800;
+ * the fused-QKV row ranges of Phi3TransformerHandler.java:329-334). */
+int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *d_x, float *const *d_y,
+                         void *stream);
+
 /* Raw-pointer variant of the quantizer: n fp32 values -> packed bytes in a
  * caller-provided device buffer of rawByteCount(type, n) bytes. */
 int jh_quantize_dev(int ggml_type, const float *d_src, int64_t n, void *d_dst, void *stream);

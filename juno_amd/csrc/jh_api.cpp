@@ -471,6 +471,55 @@ int jh_qmatvec_batched_dev(const jh_qmat *m, const float *d_X, int B, float *d_Y
     return ok();
 }
 
+int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *d_x, float *const *d_y,
+                         void *stream) {
+    if (n < 0 || n > jh::kMaxGroup) return fail(JH_EINVAL, "n=%d outside [0, %d]", n, jh::kMaxGroup);
+    if (n == 0) return ok();
+    if (!mats || !d_x || !d_y) return fail(JH_EINVAL, "mats, x and y must not be null");
+    jh::GroupProblem all[jh::kMaxGroup];
+    int rc;
+    for (int i = 0; i < n; i++) {
+        if ((rc = check_qmat(mats[i]))) return rc;
+        if (!d_x[i] || !d_y[i]) return fail(JH_EINVAL, "x[%d] and y[%d] must not be null", i, i);
+        all[i] = jh::GroupProblem{mats[i]->type, mats[i]->d_raw, mats[i]->pitch, mats[i]->cols, mats[i]->rows,
+                                  d_x[i], d_y[i], 0, 0};
+    }
+    hipStream_t s = (hipStream_t)stream;
+    bool done[jh::kMaxGroup] = {};
+    // 1. large same-format matrices sharing an x: one staged launch per class
+    for (int i = 0; i < n; i++) {
+        if (done[i] || all[i].type == JH_TYPE_F32 || gemv_path() == 1) continue;
+        jh::GroupProblem cls[jh::kMaxStagedGroup];
+        int idx[jh::kMaxStagedGroup], k = 0;
+        for (int j = i; j < n && k < jh::kMaxStagedGroup; j++)
+            if (!done[j] && all[j].type == all[i].type && all[j].cols == all[i].cols && all[j].x == all[i].x) {
+                idx[k] = j;
+                cls[k++] = all[j];
+            }
+        hipError_t e = jh::launch_gemv_staged_group(k, cls, s);
+        if (e == hipSuccess) {
+            for (int q = 0; q < k; q++) done[idx[q]] = true;
+        } else if (e != hipErrorNotSupported) {
+            return hip_fail("gemv_staged_group launch", e);
+        }
+    }
+    // 2. everything else in one launch of the one-shot kernels (F32 on its own)
+    jh::GroupArgs g = {};
+    for (int i = 0; i < n; i++) {
+        if (done[i]) continue;
+        if (all[i].type == JH_TYPE_F32) {
+            if ((rc = enqueue_matvec(mats[i], d_x[i], 1, d_y[i], 0, mats[i]->rows, s))) return rc;
+            continue;
+        }
+        g.p[g.n++] = all[i];
+    }
+    if (g.n) {
+        hipError_t e = jh::launch_gemv_group(g, s);
+        if (e != hipSuccess) return hip_fail("gemv_group launch", e);
+    }
+    return ok();
+}
+
 int jh_qmat_dequant_dev(const jh_qmat *m, float *d_out, void *stream) {
     int rc;
     if ((rc = check_qmat(m))) return rc;

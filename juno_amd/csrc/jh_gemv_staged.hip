@@ -338,16 +338,29 @@ __device__ __forceinline__ float block_dot(const XRegs<8> &x, const uint8_t *p, 
 
 // --------------------------------------------------------------------------- kernel
 
+// The kernel walks the concatenation of np matrices of one format and shape
+// class (same cols / pitch, same x): virtual row v belongs to problem p with
+// cum[p] <= v < cum[p+1] and is row row0[p] + v - cum[p] of w[p].
 struct StagedArgs {
-    const uint8_t *w;  // matrix base (row 0), 256-byte aligned (hipMalloc)
-    int row0;          // first row to compute
+    int np;
+    const uint8_t *w[kMaxStagedGroup];  // matrix bases, 256-byte aligned (hipMalloc)
+    float *y[kMaxStagedGroup];
+    int row0[kMaxStagedGroup];
+    int cum[kMaxStagedGroup + 1];
     size_t pitch;
-    int nb, nrows, cols;
+    int nb, nrows, cols;  // nrows = cum[np]
     int gw;   // waves per row group (column tiles): 1, 2 or 4
     int tb;   // blocks per tile
     const float *x;
-    float *y;
 };
+
+__device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
+    int p = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxStagedGroup; i++)
+        if (i < a.np && v >= a.cum[i]) p = i;
+    return p;
+}
 
 template <int T, int R>
 __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
@@ -394,13 +407,16 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
     // 2. weight loads.  Byte offsets are relative to args.w, which is 256-byte
     //    aligned, so a span's alignment follows from its offset alone.
     uint4 v[R][K];
-    size_t start[R];  // byte offset of each row tile of the group in flight
+    int start[R];  // misalignment (byte offset mod 16) of each row tile in flight
     auto issue = [&](int g) {
         const int r0 = min(g, ngroups - 1) * R;
 #pragma unroll
         for (int i = 0; i < R; i++) {
-            start[i] = (size_t)(args.row0 + min(r0 + i, nrows - 1)) * pitch + tile_off;
-            const uint8_t *base = args.w + (start[i] & ~size_t(15));
+            const int vr = min(r0 + i, nrows - 1);
+            const int p = staged_problem(args, vr);
+            const size_t off = (size_t)(args.row0[p] + vr - args.cum[p]) * pitch + tile_off;
+            start[i] = (int)(off & 15);
+            const uint8_t *base = args.w[p] + (off & ~size_t(15));
 #pragma unroll
             for (int k = 0; k < K; k++) v[i][k] = load_stream16(base + ld_off[k]);
         }
@@ -429,7 +445,7 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
     wave_lds_sync();
     int it = 0;
     while (true) {
-        size_t cstart[R];
+        int cstart[R];
 #pragma unroll
         for (int i = 0; i < R; i++) cstart[i] = start[i];
         const int next = grp + gstride;
@@ -439,15 +455,19 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
         float s[R];
 #pragma unroll
         for (int i = 0; i < R; i++) {
-            const uint8_t *row = cb + i * F::CH * 16 + (int)(cstart[i] & 15);
+            const uint8_t *row = cb + i * F::CH * 16 + cstart[i];
             const float d = block_dot(xr, row + lane_blk, sub);
             s[i] = wave_sum_to63(act ? d : 0.f);
         }
+        auto store = [&](int vr, float val) {
+            const int p = staged_problem(args, vr);
+            args.y[p][vr - args.cum[p]] = val;
+        };
         if (gw == 1) {
             if (lane == 63)
 #pragma unroll
                 for (int i = 0; i < R; i++)
-                    if (r0 + i < nrows) args.y[r0 + i] = s[i];
+                    if (r0 + i < nrows) store(r0 + i, s[i]);
             if (next >= ngroups) break;
         } else {
             float *pp = part + (it & 1) * 4 * R;
@@ -460,7 +480,7 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
                 for (int i = 0; i < R; i++) {
                     float t = 0.f;
                     for (int q = 0; q < gw; q++) t += pp[(slot * gw + q) * R + i];
-                    if (r0 + i < nrows) args.y[r0 + i] = t;
+                    if (r0 + i < nrows) store(r0 + i, t);
                 }
             // every wave of the workgroup iterates while slot 0 has work
             if (next - slot >= ngroups) break;
@@ -475,20 +495,12 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
 }
 
 template <int T, int R>
-hipError_t launch_staged_t(const GemvArgs &a, int nb, hipStream_t s) {
+hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
     using F = Fmt<T>;
-    StagedArgs sa;
-    sa.pitch = a.pitch;
-    sa.w = a.w;
-    sa.row0 = a.row_start;
-    sa.nb = nb;
-    sa.nrows = a.row_end - a.row_start;
-    sa.cols = a.cols;
+    const int nb = sa.nb;
     sa.gw = nb <= F::TBMAX ? 1 : nb <= 2 * F::TBMAX ? 2 : 4;
     sa.tb = (nb + sa.gw - 1) / sa.gw;
-    sa.x = a.x;
-    sa.y = a.y;
-    const int nblk = (a.cols + 255) / 256;
+    const int nblk = (sa.cols + 255) / 256;
     const size_t lds = ((XImage::bytes(nblk) + 15) & ~size_t(15)) + (size_t)4 * R * F::CH * 16 + 2 * 4 * R * 4;
     const int slots = 4 / sa.gw;
     const int ngroups = (sa.nrows + R - 1) / R;
@@ -530,29 +542,79 @@ static int staged_rows(int def) {
 }
 
 template <int T>
-static hipError_t launch_staged_r(const GemvArgs &a, int nb, int R, hipStream_t s) {
+static hipError_t launch_staged_r(const StagedArgs &sa, int R, hipStream_t s) {
     switch (R) {
-    case 1: return launch_staged_t<T, 1>(a, nb, s);
-    case 2: return launch_staged_t<T, 2>(a, nb, s);
-    default: return launch_staged_t<T, 4>(a, nb, s);
+    case 1: return launch_staged_t<T, 1>(sa, s);
+    case 2: return launch_staged_t<T, 2>(sa, s);
+    default: return launch_staged_t<T, 4>(sa, s);
+    }
+}
+
+static hipError_t launch_staged_any(const StagedArgs &sa, int type, hipStream_t s) {
+    const int R = staged_rows(2);
+    switch (type) {
+    case 12: return launch_staged_r<12>(sa, R, s);
+    case 14: return launch_staged_r<14>(sa, R, s);
+    case 8: return launch_staged_r<8>(sa, R, s);
+    default: return hipErrorNotSupported;
     }
 }
 
 // The staged kernel pays a fixed prologue (x conversion, one barrier) of a
-// few microseconds; below ~28 MB of packed weights the one-shot kernels of
-// jh_gemv.hip finish first (measured on MI355X at Llama-3-8B / Phi-3 shapes).
+// few microseconds; below ~28 MB of packed weights per launch the one-shot
+// kernels of jh_gemv.hip finish first (measured on MI355X at Llama-3-8B and
+// Phi-3 shapes).  JUNO_STAGED_R set forces the staged kernel (tests, tuning).
 constexpr size_t kStagedMinBytes = 28u << 20;
+
+static bool staged_wanted(size_t bytes) { return bytes >= kStagedMinBytes || getenv("JUNO_STAGED_R") != nullptr; }
 
 hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s) {
     if (a.batch != 1 || !staged_supported(a.type, a.cols)) return hipErrorNotSupported;
-    if ((size_t)(a.row_end - a.row_start) * a.pitch < kStagedMinBytes && !getenv("JUNO_STAGED_R"))
-        return hipErrorNotSupported;
-    switch (a.type) {
-    case 12: return launch_staged_r<12>(a, a.cols / 256, staged_rows(2), s);
-    case 14: return launch_staged_r<14>(a, a.cols / 256, staged_rows(2), s);
-    case 8: return launch_staged_r<8>(a, a.cols / 32, staged_rows(2), s);
-    default: return hipErrorNotSupported;
+    const int nrows = a.row_end - a.row_start;
+    if (!staged_wanted((size_t)nrows * a.pitch)) return hipErrorNotSupported;
+    StagedArgs sa = {};
+    sa.np = 1;
+    sa.w[0] = a.w;
+    sa.y[0] = a.y;
+    sa.row0[0] = a.row_start;
+    sa.cum[0] = 0;
+    sa.cum[1] = nrows;
+    sa.pitch = a.pitch;
+    sa.nb = a.type == 8 ? a.cols / 32 : a.cols / 256;
+    sa.nrows = nrows;
+    sa.cols = a.cols;
+    sa.x = a.x;
+    return launch_staged_any(sa, a.type, s);
+}
+
+hipError_t launch_gemv_staged_group(int n, const GroupProblem *p, hipStream_t s) {
+    if (n < 1 || n > kMaxStagedGroup) return hipErrorNotSupported;
+    size_t bytes = 0;
+    for (int i = 0; i < n; i++) {
+        if (p[i].type != p[0].type || p[i].cols != p[0].cols || p[i].pitch != p[0].pitch || p[i].x != p[0].x ||
+            !staged_supported(p[i].type, p[i].cols))
+            return hipErrorNotSupported;
+        bytes += (size_t)p[i].nrows * p[i].pitch;
     }
+    if (!staged_wanted(bytes)) return hipErrorNotSupported;
+    StagedArgs sa = {};
+    sa.np = n;
+    int total = 0;
+    for (int i = 0; i < n; i++) {
+        sa.w[i] = p[i].w;
+        sa.y[i] = p[i].y;
+        sa.row0[i] = 0;
+        sa.cum[i] = total;
+        total += p[i].nrows;
+    }
+    sa.cum[n] = total;
+    sa.pitch = p[0].pitch;
+    sa.nb = p[0].type == 8 ? p[0].cols / 32 : p[0].cols / 256;
+    sa.nrows = total;
+    sa.cols = p[0].cols;
+    sa.x = p[0].x;
+    if (total == 0) return hipSuccess;
+    return launch_staged_any(sa, p[0].type, s);
 }
 
 }  // namespace jh

@@ -27,6 +27,29 @@ struct GemvArgs {
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
 
+// Independent B = 1 GEMVs over full row ranges, one launch for all.
+constexpr int kMaxGroup = 8;
+struct GroupProblem {
+    int type;
+    const uint8_t *w;
+    size_t pitch;
+    int cols, nrows;
+    const float *x;
+    float *y;
+    int rows_per_wave, wg_begin;  // set by the launcher
+};
+struct GroupArgs {
+    int n;
+    GroupProblem p[kMaxGroup];
+};
+hipError_t launch_gemv_group(GroupArgs g, hipStream_t s);
+
+// Large same-format matrices sharing one x (e.g. gate and up) through the
+// staged kernel, as one launch over their concatenated rows.  Returns
+// hipErrorNotSupported when the problems do not qualify.
+constexpr int kMaxStagedGroup = 4;
+hipError_t launch_gemv_staged_group(int n, const GroupProblem *p, hipStream_t s);
+
 // B = 1 coalesced, pipelined, int8-x kernel (jh_gemv_staged.hip); returns
 // hipErrorNotSupported for shapes it does not cover.
 bool staged_supported(int type, int cols);

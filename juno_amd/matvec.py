@@ -280,6 +280,16 @@ class HipMatVec:
             row_end = A.rows
         _check(self._L.jh_qmatvec_batched_dev(A.handle, d_x, batch, d_y, row_start, row_end, stream or None))
 
+    def sgemv_group_dev(self, mats, d_xs, d_ys, stream: int = 0) -> None:
+        """Independent full-row GEMVs y_i = W_i x_i in as few launches as possible."""
+        n = len(mats)
+        if not (len(d_xs) == len(d_ys) == n):
+            raise IllegalArgumentException("mats, x and y must have the same length")
+        hs = (ctypes.c_void_p * max(n, 1))(*[m.handle for m in mats])
+        xs = (ctypes.c_void_p * max(n, 1))(*d_xs)
+        ys = (ctypes.c_void_p * max(n, 1))(*d_ys)
+        _check(self._L.jh_qmatvec_group_dev(n, hs, xs, ys, stream or None))
+
     def dequantize_dev(self, A: DeviceQuantMatrix, d_out: int, stream: int = 0) -> None:
         _check(self._L.jh_qmat_dequant_dev(A.handle, d_out, stream or None))
 

@@ -394,3 +394,39 @@ def test_llama8b_shapes_full_size(be):
         lin = 0.5 * y1.astype(np.float64) + 2.0 * y2.astype(np.float64)
         xs = np.abs(x1) * 0.5 + np.abs(x2) * 2.0
         assert rel_err(y12, lin, deq, xs).max() <= 2 * TOL
+
+
+def test_group_dev_matches_single_calls(be):
+    """jh_qmatvec_group_dev: q, k (Q4_K) + v (Q6_K) sharing x, gate + up (Q4_K,
+    >= 28 MB together -> one staged launch), a Q8_0 and an F32 matrix with their
+    own x; each output equals the oracle to the GEMV bar."""
+    import torch
+    specs = [("q", O.Q4_K, 4096, 4096, 0), ("k", O.Q4_K, 1024, 4096, 0), ("v", O.Q6_K, 1024, 4096, 0),
+             ("gate", O.Q4_K, 14336, 4096, 1), ("up", O.Q4_K, 14336, 4096, 1),
+             ("q8", O.Q8_0, 777, 3072, 2), ("f32", O.F32, 100, 384, 3)]
+    xs = {0: vec(4096, 200), 1: vec(4096, 201), 2: vec(3072, 202), 3: vec(384, 203)}
+    dxs = {k: torch.from_numpy(v).cuda() for k, v in xs.items()}
+    mats, raws, dys = [], [], []
+    for name, qt, rows, cols, xi in specs:
+        say("group", name)
+        raw = O.quantize(qt, weights(rows * cols, 300 + rows + qt))
+        raws.append(raw)
+        mats.append(upload(be, qt, raw, rows, cols))
+        dys.append(torch.full((rows,), float("nan"), device="cuda"))
+    be.sgemv_group_dev(mats, [dxs[s[4]].data_ptr() for s in specs], [y.data_ptr() for y in dys])
+    torch.cuda.synchronize()
+    for (name, qt, rows, cols, xi), raw, dy, m in zip(specs, raws, dys, mats):
+        y = dy.cpu().numpy()
+        ref = O.matvec(qt, raw, xs[xi], 0, rows, cols).astype(np.float64)
+        deq = O.dequantize(qt, raw, rows, cols)
+        assert rel_err(y, ref, deq, xs[xi]).max() <= TOL, name
+        m.close()
+
+
+def test_group_dev_arguments(be):
+    from juno_amd import _lib
+    L = _lib.load()
+    assert L.jh_qmatvec_group_dev(9, None, None, None, None) == _lib.JH_EINVAL
+    assert "n=9" in _lib.last_error()
+    assert L.jh_qmatvec_group_dev(1, None, None, None, None) == _lib.JH_EINVAL
+    be.sgemv_group_dev([], [], [])  # n = 0 is a no-op
