@@ -261,6 +261,55 @@ def parity_spot_check(torch, L, mats, stream):
     return float((np.abs(y - ref) / np.maximum(np.abs(ref), 1e-3 * scale)).max())
 
 
+def profile_mode(torch, L, be):
+    """Launches for hardware-counter runs (rocprofv3 --pmc): 8 layers' grouped
+    [gate, up] Q4_K GEMVs, eagerly, 4 times each, then the calibration copy."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    mats = []
+    for layer in range(8):
+        pair = []
+        for name in ("ffn_gate", "ffn_up"):
+            w = torch.randn(FFN * HIDDEN, generator=g, device="cuda").mul_(0.02)
+            pair.append(be.quantize_dev(Q4_K, w.data_ptr(), FFN, HIDDEN, torch.cuda.current_stream().cuda_stream))
+            del w
+        mats.append(pair)
+    torch.cuda.synchronize()
+    x = torch.randn(HIDDEN, device="cuda")
+    ys = [torch.empty(FFN, device="cuda") for _ in range(2)]
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for _ in range(4):
+        for ga, ua in mats:
+            hs = (ctypes.c_void_p * 2)(ga.handle, ua.handle)
+            xp = (ctypes.c_void_p * 2)(x.data_ptr(), x.data_ptr())
+            yp = (ctypes.c_void_p * 2)(ys[0].data_ptr(), ys[1].data_ptr())
+            if L.jh_qmatvec_group_dev(2, hs, xp, yp, s):
+                raise RuntimeError(L.jh_last_error().decode())
+    torch.cuda.synchronize()
+    # calibration: an elementwise kernel that reads 1 GiB and writes 1 GiB
+    a = torch.empty(1 << 28, device="cuda")
+    a.fill_(1.0)
+    b = torch.empty_like(a)
+    torch.mul(a, 2.0, out=b)
+    torch.cuda.synchronize()
+    per_launch = 2 * packed_bytes(FFN, HIDDEN, Q4_K) + 4 * (HIDDEN + 2 * FFN)
+    print(json.dumps({"profile": "gemv_staged Q4_K [gate, up]", "launches": 32,
+                      "algorithmic_bytes_per_launch": per_launch,
+                      "calibration": "torch.mul 2^28 fp32: reads 1073741824 B, writes 1073741824 B"}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    --pmc summary (FETCH_SIZE + WRITE_SIZE, calibrated; see profiles/)."""
+    p = os.path.join(ROOT, "profiles", "gemv_staged_q4k_gate_up_counters.json")
+    try:
+        with open(p) as f:
+            d = json.load(f)
+        return int(d["traffic_bytes_per_launch"]), "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE (profiles/gemv_staged_q4k_gate_up_counters.json)"
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -269,6 +318,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
+    ap.add_argument("--profile", action="store_true",
+                    help="counter-collection mode: only the dominant kernel (eager launches over 8 layers' "
+                         "[gate, up]) and a 1 GiB elementwise copy that calibrates FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -284,6 +336,9 @@ def main():
     be = ctx.create_mat_vec()
     info = mv.device_info(0)
     log(f"device {info}")
+    if args.profile:
+        profile_mode(torch, L, be)
+        return
     t0 = time.perf_counter()
     mats = build_model(torch, be)
     log(f"model built: {len(mats)} matrices, {sum(m[4].nbytes() for m in mats) / 1e9:.3f} GB packed, "
@@ -310,6 +365,7 @@ def main():
                    "GB_s": round(sb32 / (ms32 * 1e-3) / 1e9, 1)}
         log(f"B=32 step: {ms32:.4f} ms  {batched}")
 
+    traffic, traffic_src = measured_traffic()
     parity = parity_spot_check(torch, L, mats, stream)
     log(f"parity spot check (layer-0 gate vs oracle): max rel-err {parity:.2e}")
 
@@ -338,7 +394,7 @@ def main():
         "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
         "tok_s": round(1e3 / ms, 1),
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": "gemv_staged<Q4_K> [gate, up] 2x14336x4096 B=1 (one launch)",
                      "avg_launch_us": round(avg_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": per_launch},
