@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 
@@ -172,6 +173,32 @@ int check_range(const jh_qmat *m, int row_start, int row_end) {
 
 int gemv_path();
 
+// Device workspace of the batched MFMA path, one per (device, stream): work on
+// one stream is ordered, so a stream's launches never overlap in it.  Sized on
+// first use (at least 8 MB) and grown if needed; growth frees the old buffer
+// after a device synchronisation, so size it with an eager call before graph
+// capture.  Released at process exit.
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> g_ws;
+
+int stream_workspace(int device, hipStream_t s, size_t bytes, void **out) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto &e = g_ws[{device, s}];
+    if (e.second < bytes) {
+        if (e.first) {
+            (void)hipDeviceSynchronize();
+            (void)hipFree(e.first);
+            e = {nullptr, 0};
+        }
+        size_t want = bytes < (8u << 20) ? (8u << 20) : bytes;
+        int rc = device_alloc(&e.first, want);
+        if (rc) return rc;
+        e.second = want;
+    }
+    *out = e.first;
+    return JH_OK;
+}
+
 // Enqueue y = W x for B vectors (device pointers), splitting B into the
 // kernel's supported batch widths, or using the MFMA path for B >= 16.
 int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int row_start, int row_end,
@@ -188,12 +215,18 @@ int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int ro
     a.ldx = m->cols;
     a.ldy = nrows;
     if (B >= 16) {
-        a.batch = B;
-        a.x = d_x;
-        a.y = d_y;
-        hipError_t rc = jh::launch_gemm_mfma(a, s);
-        if (rc == hipSuccess) return JH_OK;
-        if (rc != hipErrorNotSupported) return hip_fail("gemm_mfma launch", rc);
+        const size_t wsb = jh::mfma_workspace_bytes(m->type, B, m->cols);
+        if (wsb) {
+            void *ws = nullptr;
+            int rc = stream_workspace(m->ctx->device, s, wsb, &ws);
+            if (rc) return rc;
+            a.batch = B;
+            a.x = d_x;
+            a.y = d_y;
+            hipError_t e = jh::launch_gemm_mfma_ws(a, ws, s);
+            if (e == hipSuccess) return JH_OK;
+            if (e != hipErrorNotSupported) return hip_fail("gemm_mfma launch", e);
+        }
     }
     if (B == 1 && gemv_path() != 1) {
         a.batch = 1;

@@ -55,9 +55,12 @@ hipError_t launch_gemv_staged_group(int n, const GroupProblem *p, hipStream_t s)
 bool staged_supported(int type, int cols);
 hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s);
 
-// Batched decode through the LDS-dequant + fp16 MFMA path (B >= 16).
-// Returns hipErrorNotSupported for types without an MFMA kernel.
-hipError_t launch_gemm_mfma(const GemvArgs &a, hipStream_t s);
+// Batched decode through the LDS-staged, fp16-MFMA path (16 <= B <= 64).
+// mfma_workspace_bytes returns 0 when the path does not apply (type / shape);
+// otherwise launch_gemm_mfma_ws needs that many bytes of device workspace,
+// which must not be in use by another stream while the launch runs.
+size_t mfma_workspace_bytes(int type, int B, int cols);
+hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s);
 
 // out[rows][cols] fp32, bit-exact with the reference dequantizers.
 hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float *out, hipStream_t s);

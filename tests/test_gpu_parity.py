@@ -231,7 +231,7 @@ def test_x_not_mutated(be):
     assert np.array_equal(x, x0)
 
 
-@pytest.mark.parametrize("B", [1, 2, 3, 5, 8, 11, 16, 32])
+@pytest.mark.parametrize("B", [1, 2, 3, 5, 8, 11, 16, 20, 32, 48, 64])
 @pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.Q8_0])
 def test_batched_vs_independent(be, qtype, B):
     rows, cols = 1024, 2048
@@ -247,6 +247,23 @@ def test_batched_vs_independent(be, qtype, B):
         ref = O.matvec(qtype, raw, X[j], 0, rows, cols)
         assert rel_err(Y[j], ref.astype(np.float64), deq, X[j]).max() <= TOL, j
     assert rel_err(y1, Y[-1].astype(np.float64), deq, X[-1]).max() <= TOL
+
+
+def test_batched_mfma_8b_shapes(be):
+    """The MFMA path at Llama-3-8B shapes (gate 14336x4096: no K split; k 1024x4096:
+    K split with atomics), B in {16, 32, 64}, against the oracle per column."""
+    for rows, cols in [(14336, 4096), (1024, 4096)]:
+        raw = O.quantize(O.Q4_K, weights(rows * cols, 400 + rows))
+        deq = O.dequantize(O.Q4_K, raw, rows, cols)
+        with upload(be, O.Q4_K, raw, rows, cols) as dev:
+            for B in (16, 32, 64):
+                say("mfma", rows, cols, B)
+                X = vec(cols, 500 + B, batch=B)
+                X[:, ::131] *= 30.0
+                Y = be.sgemv_batched(dev, X)
+                for j in (0, B // 2, B - 1):
+                    ref = O.matvec(O.Q4_K, raw, X[j], 0, rows, cols).astype(np.float64)
+                    assert rel_err(Y[j], ref, deq, X[j]).max() <= TOL, (rows, B, j)
 
 
 def test_batched_row_range(be):
