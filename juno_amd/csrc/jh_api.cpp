@@ -215,7 +215,7 @@ int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int ro
     a.ldx = m->cols;
     a.ldy = nrows;
     if (B >= 16) {
-        const size_t wsb = jh::mfma_workspace_bytes(m->type, B, m->cols);
+        const size_t wsb = jh::mfma_workspace_bytes(m->type, B, m->cols, row_end - row_start);
         if (wsb) {
             void *ws = nullptr;
             int rc = stream_workspace(m->ctx->device, s, wsb, &ws);

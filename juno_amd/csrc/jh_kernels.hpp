@@ -58,8 +58,9 @@ hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s);
 // Batched decode through the LDS-staged, fp16-MFMA path (16 <= B <= 64).
 // mfma_workspace_bytes returns 0 when the path does not apply (type / shape);
 // otherwise launch_gemm_mfma_ws needs that many bytes of device workspace,
-// which must not be in use by another stream while the launch runs.
-size_t mfma_workspace_bytes(int type, int B, int cols);
+// which must not be in use by another stream while the launch runs (its
+// contents need not be initialised).
+size_t mfma_workspace_bytes(int type, int B, int cols, int rows);
 hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s);
 
 // out[rows][cols] fp32, bit-exact with the reference dequantizers.

@@ -21,8 +21,11 @@
 //  * Work split: a workgroup is 4 waves x 32 rows = 128 rows, all B columns,
 //    and a range of super-blocks.  Every x fragment staged in LDS feeds 128
 //    rows (operand traffic ~3.5x the weight bytes at B = 32, within LDS
-//    bandwidth).  When the row tiles are too few to fill 256 CUs the K range is
-//    split across workgroups and the partial sums meet through fp32 atomics.
+//    bandwidth).  The next super-block's weights and x slice are loaded while
+//    the current one is multiplied.  When the row tiles are too few to fill
+//    256 CUs the K range is split across workgroups; each split writes its
+//    partial tile to the workspace and a small kernel adds the partials in
+//    split order (deterministic; no float atomics).
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
 
@@ -31,6 +34,8 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kMinWorkgroups = 512;  // split K until the grid has this many
 
 constexpr int kRowsPerWave = 32;
 constexpr int kRowsPerWG = 4 * kRowsPerWave;
@@ -39,17 +44,24 @@ constexpr int kXPad = 8;  // halves of padding per LDS column (spreads banks)
 // ------------------------------------------------------------------ workspace layout
 struct XWork {
     int Bp, cols, nsb;  // padded batch, columns, super-blocks (cols / 256)
+    int rows, ksplit;  // split-K partials: [ksplit][B][rows] f32
     uint8_t *base;
-    __host__ __device__ size_t hi_off() const { return 0; }
-    __host__ __device__ size_t lo_off() const { return (size_t)Bp * cols * 2; }
-    __host__ __device__ size_t xs_off() const { return (size_t)Bp * cols * 4; }            // [Bp][nsb][16] halves
-    __host__ __device__ size_t s_off() const { return xs_off() + (size_t)Bp * nsb * 32; }  // [Bp][nsb] f32
-    __host__ __device__ size_t sc_off() const { return s_off() + (size_t)Bp * nsb * 4; }   // [Bp] f32
-    __host__ __device__ size_t bytes() const { return sc_off() + (size_t)Bp * 4; }
-    __device__ _Float16 *hi() const { return reinterpret_cast<_Float16 *>(base + hi_off()); }
-    __device__ _Float16 *lo() const { return reinterpret_cast<_Float16 *>(base + lo_off()); }
-    __device__ _Float16 *xs() const { return reinterpret_cast<_Float16 *>(base + xs_off()); }
-    __device__ float *S() const { return reinterpret_cast<float *>(base + s_off()); }
+    // The prepared x is super-block major: one contiguous slab per super-block,
+    //   [hi: Bp x 256 halves][lo: Bp x 256 halves][xs: Bp x 16 halves][S: Bp f32]
+    // so the slice every workgroup stages for a super-block is one linear
+    // stretch of memory (a column-major image would put the 32 column segments
+    // of a slice a power-of-two stride apart, on the same memory channels).
+    __host__ __device__ size_t slab() const { return ((size_t)Bp * 1060 + 255) & ~size_t(255); }
+    __host__ __device__ size_t x_off() const { return 0; }
+    __host__ __device__ size_t sc_off() const { return x_off() + slab() * nsb; }  // [Bp] f32
+    __host__ __device__ size_t part_off() const { return (sc_off() + (size_t)Bp * 4 + 255) & ~size_t(255); }
+    __host__ __device__ size_t bytes() const { return part_off() + (ksplit > 1 ? (size_t)ksplit * Bp * rows * 4 : 0); }  // [ksplit][B][rows]
+    __device__ float *part() const { return reinterpret_cast<float *>(base + part_off()); }
+    __device__ uint8_t *sbx(int sb) const { return base + x_off() + slab() * sb; }
+    __device__ _Float16 *hi(int sb) const { return reinterpret_cast<_Float16 *>(sbx(sb)); }
+    __device__ _Float16 *lo(int sb) const { return reinterpret_cast<_Float16 *>(sbx(sb) + (size_t)Bp * 512); }
+    __device__ _Float16 *xs(int sb) const { return reinterpret_cast<_Float16 *>(sbx(sb) + (size_t)Bp * 1024); }
+    __device__ float *S(int sb) const { return reinterpret_cast<float *>(sbx(sb) + (size_t)Bp * 1056); }
     __device__ float *scale() const { return reinterpret_cast<float *>(base + sc_off()); }
 };
 
@@ -87,9 +99,9 @@ __global__ __launch_bounds__(256) void x_prep_mfma(const float *__restrict__ X, 
     if (m > 0.f) (void)frexpf(m, &e);
     const float s = m > 0.f ? ldexpf(1.f, 13 - e) : 1.f;
     if (threadIdx.x == 0) w.scale()[b] = 1.f / s;
-    _Float16 *hi = w.hi() + (size_t)b * cols, *lo = w.lo() + (size_t)b * cols;
     for (int sb = wave; sb < w.nsb; sb += 4) {
         const int c = sb * 256 + lane * 4;
+        _Float16 *hi = w.hi(sb) + (size_t)b * 256 + lane * 4, *lo = w.lo(sb) + (size_t)b * 256 + lane * 4;
         float4 v = real ? *reinterpret_cast<const float4 *>(xb + c) : make_float4(0.f, 0.f, 0.f, 0.f);
         const float e4[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
         float sum = 0.f;
@@ -97,8 +109,8 @@ __global__ __launch_bounds__(256) void x_prep_mfma(const float *__restrict__ X, 
         for (int j = 0; j < 4; j++) {
             const _Float16 h = (_Float16)e4[j];
             const _Float16 l = (_Float16)(e4[j] - (float)h);
-            hi[c + j] = h;
-            lo[c + j] = l;
+            hi[j] = h;
+            lo[j] = l;
             sum += (float)h + (float)l;
         }
         // sub-block (32 columns = 8 lanes) sums, and the super-block sum
@@ -107,27 +119,23 @@ __global__ __launch_bounds__(256) void x_prep_mfma(const float *__restrict__ X, 
         sub += __shfl_xor(sub, 2);
         sub += __shfl_xor(sub, 4);
         const float tot = wave_reduce_sum(sum);
-        _Float16 *xs = w.xs() + ((size_t)b * w.nsb + sb) * 16;
+        _Float16 *xs = w.xs(sb) + (size_t)b * 16;
         if ((lane & 7) == 0) {
             const _Float16 h = (_Float16)sub;
             xs[lane >> 3] = h;
             xs[8 + (lane >> 3)] = (_Float16)(sub - (float)h);
         }
-        if (lane == 0) w.S()[(size_t)b * w.nsb + sb] = tot;
+        if (lane == 0) w.S(sb)[b] = tot;
     }
-}
-
-__global__ __launch_bounds__(256) void fill_zero(float *__restrict__ y, size_t n) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) y[i] = 0.f;
 }
 
 // ------------------------------------------------------------------ Q4_K batched kernel
 template <int NT>  // NT = padded batch / 32
 __global__ __launch_bounds__(256) void mfma_q4k(const uint8_t *__restrict__ W, size_t pitch, int row0, int nrows,
-                                                int nsb, int ksb, XWork xw, float *__restrict__ Y, int B,
-                                                bool atomic) {
+                                                int nsb, int ksb, XWork xw, float *__restrict__ Y, int B) {
     constexpr int BP = 32 * NT;
-    constexpr int COLH = 256 + kXPad;  // halves per LDS column
+    constexpr int COLH = 256 + kXPad;   // halves per LDS column
+    constexpr int XU = BP * 32 / 256;   // 16-byte x units per thread per limb
     __shared__ __align__(16) _Float16 sh_hi[BP * COLH];
     __shared__ __align__(16) _Float16 sh_lo[BP * COLH];
     __shared__ __align__(16) _Float16 sh_xs[BP * 16];
@@ -142,42 +150,66 @@ __global__ __launch_bounds__(256) void mfma_q4k(const uint8_t *__restrict__ W, s
     const uint8_t *rowp = W + (size_t)(row0 + myrow) * pitch;
     const int sb0 = blockIdx.y * ksb, sb1 = min(nsb, sb0 + ksb);
 
+    // register sets for the next super-block: x slice units and weight bytes
+    u32x4 xh_n[XU], xl_n[XU], xs_n;
+    float S_n = 0.f;
+    u32x4 hd_n;
+    u32x2 qp_n[4][2];
+    // (macros rather than lambdas: the register arrays must stay in VGPRs)
+#define JH_LOAD_X(SB)                                                                                     \
+    do {                                                                                                  \
+        const u32x4 *hp = reinterpret_cast<const u32x4 *>(xw.hi(SB));                                    \
+        const u32x4 *lp = reinterpret_cast<const u32x4 *>(xw.lo(SB));                                    \
+        _Pragma("unroll") for (int k = 0; k < XU; k++) {                                                  \
+            xh_n[k] = hp[threadIdx.x + 256 * k];                                                          \
+            xl_n[k] = lp[threadIdx.x + 256 * k];                                                          \
+        }                                                                                                 \
+        xs_n = reinterpret_cast<const u32x4 *>(xw.xs(SB))[min((int)threadIdx.x, BP * 2 - 1)];            \
+        S_n = xw.S(SB)[min((int)threadIdx.x, BP - 1)];                                                    \
+    } while (0)
+#define JH_LOAD_W(SB)                                                                                     \
+    do {                                                                                                  \
+        const uint8_t *bp = rowp + (size_t)(SB) * 144;                                                    \
+        hd_n = *reinterpret_cast<const u32x4 *>(bp);                                                      \
+        _Pragma("unroll") for (int g = 0; g < 4; g++) {                                                   \
+            qp_n[g][0] = *reinterpret_cast<const u32x2 *>(bp + 16 + 32 * g + 8 * kh);                     \
+            qp_n[g][1] = *reinterpret_cast<const u32x2 *>(bp + 16 + 32 * g + 16 + 8 * kh);                \
+        }                                                                                                 \
+    } while (0)
+
     f32x16 tot[NT];
 #pragma unroll
     for (int n = 0; n < NT; n++) tot[n] = (f32x16){};
 
+    if (sb0 < sb1) {
+        JH_LOAD_X(sb0);  // x first: waiting for it must not wait for the weight stream
+        JH_LOAD_W(sb0);
+    }
     for (int sb = sb0; sb < sb1; sb++) {
-        // weight bytes of this lane's row: header + 4 groups x 2 pieces of 8 bytes
-        const uint8_t *bp = rowp + (size_t)sb * 144;
-        const uint4 hd = *reinterpret_cast<const uint4 *>(bp);
-        uint2 qp[4][2];
+        __syncthreads();  // the previous super-block's LDS slice is consumed
+#pragma unroll
+        for (int k = 0; k < XU; k++) {
+            const int i = threadIdx.x + 256 * k, col = i >> 5, u = i & 31;
+            *reinterpret_cast<u32x4 *>(sh_hi + col * COLH + 8 * u) = xh_n[k];
+            *reinterpret_cast<u32x4 *>(sh_lo + col * COLH + 8 * u) = xl_n[k];
+        }
+        if (threadIdx.x < BP * 2) *reinterpret_cast<u32x4 *>(sh_xs + (threadIdx.x >> 1) * 16 + 8 * (threadIdx.x & 1)) = xs_n;
+        if (threadIdx.x < BP) sh_S[threadIdx.x] = S_n;
+        const u32x4 hd = hd_n;
+        u32x2 qp[4][2];
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            qp[g][0] = *reinterpret_cast<const uint2 *>(bp + 16 + 32 * g + 8 * kh);
-            qp[g][1] = *reinterpret_cast<const uint2 *>(bp + 16 + 32 * g + 16 + 8 * kh);
-        }
-        __syncthreads();  // previous super-block's x slice is consumed
-        // stage this super-block's x slice: BP columns x 256 halves, hi and lo
-        {
-            const size_t gbase = (size_t)sb * 256;
-            for (int i = threadIdx.x; i < BP * 32; i += 256) {  // 16-byte units: 32 per column
-                const int col = i >> 5, u = i & 31;
-                const uint4 h = *reinterpret_cast<const uint4 *>(xw.hi() + (size_t)col * xw.cols + gbase + 8 * u);
-                const uint4 l = *reinterpret_cast<const uint4 *>(xw.lo() + (size_t)col * xw.cols + gbase + 8 * u);
-                *reinterpret_cast<uint4 *>(sh_hi + col * COLH + 8 * u) = h;
-                *reinterpret_cast<uint4 *>(sh_lo + col * COLH + 8 * u) = l;
-            }
-            for (int i = threadIdx.x; i < BP * 2; i += 256) {
-                const int col = i >> 1, u = i & 1;
-                *reinterpret_cast<uint4 *>(sh_xs + col * 16 + 8 * u) =
-                    *reinterpret_cast<const uint4 *>(xw.xs() + ((size_t)col * nsb + sb) * 16 + 8 * u);
-            }
-            for (int i = threadIdx.x; i < BP; i += 256) sh_S[i] = xw.S()[(size_t)i * nsb + sb];
+            qp[g][0] = qp_n[g][0];
+            qp[g][1] = qp_n[g][1];
         }
         const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
         if (kh == 0) {
             sh_d[wave][lr] = d;
             sh_dm[wave][lr] = dmin;
+        }
+        if (sb + 1 < sb1) {  // prefetch the next super-block during this one's math
+            JH_LOAD_X(sb + 1);
+            JH_LOAD_W(sb + 1);
         }
         __syncthreads();
 
@@ -198,12 +230,12 @@ __global__ __launch_bounds__(256) void mfma_q4k(const uint8_t *__restrict__ W, s
         for (int t = 0; t < 16; t++) {
             // K-step t covers sub-block s = t/2, elements 16*(t&1) + 8*kh .. +8
             const int s = t >> 1, g = s >> 1, hiN = s & 1;
-            const uint2 q = qp[g][t & 1];
+            const u32x2 q = qp[g][t & 1];
             const uint32_t nib0 = hiN ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
             const uint32_t nib1 = hiN ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
             // pairs (e0,e1),(e2,e3),... as 16-bit lanes; then 0x6400 + ls*q per lane
             uint32_t pr[4];
-            pr[0] = __builtin_amdgcn_perm(0u, nib0, 0x0C010C00u);  // bytes: e0 | e1 << 16
+            pr[0] = __builtin_amdgcn_perm(0u, nib0, 0x0C010C00u);  // e0 | e1 << 16
             pr[1] = __builtin_amdgcn_perm(0u, nib0, 0x0C030C02u);
             pr[2] = __builtin_amdgcn_perm(0u, nib1, 0x0C010C00u);
             pr[3] = __builtin_amdgcn_perm(0u, nib1, 0x0C030C02u);
@@ -246,29 +278,70 @@ __global__ __launch_bounds__(256) void mfma_q4k(const uint8_t *__restrict__ W, s
             }
         }
     }
-    // write Y[b][row] (scaled back by the column's power of two)
+
+#undef JH_LOAD_X
+#undef JH_LOAD_W
+
+    // results, scaled back by the column's power of two
+    const int ksplit = gridDim.y;
+    if (ksplit == 1) {
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const int col = n * 32 + lr;
+            if (col >= B) continue;
+            const float cs = xw.scale()[col];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int r = rbase + (i >> 2) * 8 + 4 * kh + (i & 3);
+                if (r < nrows) Y[(size_t)col * nrows + r] = tot[n][i] * cs;
+            }
+        }
+        return;
+    }
+    // split K: each split writes its partial tile; reduce_splits adds them in
+    // split order (deterministic).  A cross-workgroup hand-off inside this
+    // kernel would need a device-scope release per workgroup, which on a
+    // multi-XCD part writes back the whole L2 each time (~100 us measured).
+    float *part = xw.part() + (size_t)blockIdx.y * B * nrows;
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const int col = n * 32 + lr;
         if (col >= B) continue;
-        const float cs = xw.scale()[col];
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = rbase + (i >> 2) * 8 + 4 * kh + (i & 3);
-            if (r >= nrows) continue;
-            float *dst = Y + (size_t)col * nrows + r;
-            const float v = tot[n][i] * cs;
-            if (atomic) atomicAdd(dst, v);
-            else *dst = v;
+            if (r < nrows) part[(size_t)col * nrows + r] = tot[n][i];
         }
+    }
+}
+
+// y[c][r] = scale[c] * sum over splits k (in order) of part[k][c][r]
+__global__ __launch_bounds__(256) void reduce_splits(XWork xw, int B, int nrows, int ksplit, float *__restrict__ Y) {
+    const size_t n = (size_t)B * nrows;
+    const float *p = xw.part();
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        float v = 0.f;
+        for (int k = 0; k < ksplit; k++) v += p[(size_t)k * n + i];
+        Y[i] = v * xw.scale()[i / nrows];
     }
 }
 
 }  // namespace
 
-size_t mfma_workspace_bytes(int type, int B, int cols) {
-    if (type != 12 || B < 16 || B > 64 || cols % 256) return 0;
-    XWork w{(B + 31) / 32 * 32, cols, cols / 256, nullptr};
+static void mfma_split(int nrows, int nsb, int &tiles, int &ksplit, int &ksb) {
+    tiles = (nrows + kRowsPerWG - 1) / kRowsPerWG;
+    ksplit = (kMinWorkgroups + tiles - 1) / tiles;
+    if (ksplit > nsb) ksplit = nsb;
+    if (ksplit < 1) ksplit = 1;
+    ksb = (nsb + ksplit - 1) / ksplit;
+    ksplit = (nsb + ksb - 1) / ksb;
+}
+
+size_t mfma_workspace_bytes(int type, int B, int cols, int rows) {
+    if (type != 12 || B < 16 || B > 64 || cols % 256 || rows < 1) return 0;
+    int tiles, ksplit, ksb;
+    mfma_split(rows, cols / 256, tiles, ksplit, ksb);
+    XWork w{(B + 31) / 32 * 32, cols, cols / 256, rows, ksplit, nullptr};
     return w.bytes();
 }
 
@@ -276,30 +349,23 @@ hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s
     if (a.type != 12 || a.batch < 16 || a.batch > 64 || a.cols % 256) return hipErrorNotSupported;
     const int B = a.batch, Bp = (B + 31) / 32 * 32;
     const int nrows = a.row_end - a.row_start;
-    XWork w{Bp, a.cols, a.cols / 256, reinterpret_cast<uint8_t *>(workspace)};
+    const int nsb = a.cols / 256;
+    int tiles, ksplit, ksb;
+    mfma_split(nrows, nsb, tiles, ksplit, ksb);
+    XWork w{Bp, a.cols, nsb, nrows, ksplit, reinterpret_cast<uint8_t *>(workspace)};
     x_prep_mfma<<<Bp, 256, 0, s>>>(a.x, B, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int tiles = (nrows + kRowsPerWG - 1) / kRowsPerWG;
-    const int nsb = a.cols / 256;
-    int ksplit = (512 + tiles - 1) / tiles;
-    if (ksplit > nsb) ksplit = nsb;
-    if (ksplit < 1) ksplit = 1;
-    const int ksb = (nsb + ksplit - 1) / ksplit;
-    ksplit = (nsb + ksb - 1) / ksb;
-    const bool atomic = ksplit > 1;
-    if (atomic) {
-        const size_t n = (size_t)B * nrows;
-        fill_zero<<<(unsigned)((n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048), 256, 0, s>>>(a.y, n);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
     dim3 grid(tiles, ksplit);
     if (Bp == 32)
-        mfma_q4k<1><<<grid, 256, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B, atomic);
+        mfma_q4k<1><<<grid, 256, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B);
     else
-        mfma_q4k<2><<<grid, 256, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B, atomic);
+        mfma_q4k<2><<<grid, 256, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B);
+    e = hipGetLastError();
+    if (e != hipSuccess || ksplit == 1) return e;
+    const size_t n = (size_t)B * nrows;
+    reduce_splits<<<(unsigned)std::min<size_t>((n + 255) / 256, 2048), 256, 0, s>>>(w, B, nrows, ksplit, a.y);
     return hipGetLastError();
 }
-
 
 }  // namespace jh
