@@ -35,6 +35,11 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// 2-byte-aligned views for Q6_K / Q8_0 fields (gfx950 global loads take any
+// byte address; the compiler still emits single dwordx2 / dwordx4 loads)
+typedef uint32_t u32x2a2 __attribute__((ext_vector_type(2), aligned(2)));
+typedef uint32_t u32x4a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32a2 __attribute__((aligned(2)));
 constexpr int kMinWorkgroups = 512;  // split K until the grid has this many
 
 constexpr int kRowsPerWave = 32;
@@ -47,22 +52,20 @@ struct XWork {
     int rows, ksplit;  // split-K partials: [ksplit][B][rows] f32
     uint8_t *base;
     // The prepared x is super-block major: one contiguous slab per super-block,
-    //   [hi: Bp x 256 halves][lo: Bp x 256 halves][xs: Bp x 16 halves][S: Bp f32]
+    //   [hi: Bp x 256 halves][lo: Bp x 256 halves][xs: Bp x 16 halves][SI: Bp x (S, 1/scale) f32]
     // so the slice every workgroup stages for a super-block is one linear
     // stretch of memory (a column-major image would put the 32 column segments
     // of a slice a power-of-two stride apart, on the same memory channels).
-    __host__ __device__ size_t slab() const { return ((size_t)Bp * 1060 + 255) & ~size_t(255); }
+    __host__ __device__ size_t slab() const { return ((size_t)Bp * 1064 + 255) & ~size_t(255); }
     __host__ __device__ size_t x_off() const { return 0; }
-    __host__ __device__ size_t sc_off() const { return x_off() + slab() * nsb; }  // [Bp] f32
-    __host__ __device__ size_t part_off() const { return (sc_off() + (size_t)Bp * 4 + 255) & ~size_t(255); }
+    __host__ __device__ size_t part_off() const { return x_off() + slab() * nsb; }
     __host__ __device__ size_t bytes() const { return part_off() + (ksplit > 1 ? (size_t)ksplit * Bp * rows * 4 : 0); }  // [ksplit][B][rows]
     __device__ float *part() const { return reinterpret_cast<float *>(base + part_off()); }
     __device__ uint8_t *sbx(int sb) const { return base + x_off() + slab() * sb; }
     __device__ _Float16 *hi(int sb) const { return reinterpret_cast<_Float16 *>(sbx(sb)); }
     __device__ _Float16 *lo(int sb) const { return reinterpret_cast<_Float16 *>(sbx(sb) + (size_t)Bp * 512); }
     __device__ _Float16 *xs(int sb) const { return reinterpret_cast<_Float16 *>(sbx(sb) + (size_t)Bp * 1024); }
-    __device__ float *S(int sb) const { return reinterpret_cast<float *>(sbx(sb) + (size_t)Bp * 1056); }
-    __device__ float *scale() const { return reinterpret_cast<float *>(base + sc_off()); }
+    __device__ float2 *SI(int sb) const { return reinterpret_cast<float2 *>(sbx(sb) + (size_t)Bp * 1056); }
 };
 
 __device__ __forceinline__ float wave_reduce_max(float v) {
@@ -76,86 +79,314 @@ __device__ __forceinline__ float wave_reduce_sum(float v) {
     return v;
 }
 
-// One workgroup per (padded) batch column.
+// One wave per (padded batch column, super-block): a power-of-two scale per
+// super-block puts max |x s| in [2^12, 2^13) (exact, undone on the partial
+// sums), then the hi/lo split and the sub-block and super-block sums.
 __global__ __launch_bounds__(256) void x_prep_mfma(const float *__restrict__ X, int B, XWork w) {
-    __shared__ float red[4];
-    const int b = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int cols = w.cols;
-    const float *xb = X + (size_t)b * cols;
-    const bool real = b < B;
-    float m = 0.f;
-    if (real)
-        for (int c = threadIdx.x * 4; c < cols; c += 1024) {
-            const float4 v = *reinterpret_cast<const float4 *>(xb + c);
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        }
-    m = wave_reduce_max(m);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    // power-of-two scale: max |x * s| in [2^12, 2^13); exact, and undone on y
+    const int lane = threadIdx.x & 63;
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), sb = blockIdx.y;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (b < B) v = *reinterpret_cast<const float4 *>(X + (size_t)b * w.cols + sb * 256 + lane * 4);
+    const float m = wave_reduce_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);
     const float s = m > 0.f ? ldexpf(1.f, 13 - e) : 1.f;
-    if (threadIdx.x == 0) w.scale()[b] = 1.f / s;
-    for (int sb = wave; sb < w.nsb; sb += 4) {
-        const int c = sb * 256 + lane * 4;
-        _Float16 *hi = w.hi(sb) + (size_t)b * 256 + lane * 4, *lo = w.lo(sb) + (size_t)b * 256 + lane * 4;
-        float4 v = real ? *reinterpret_cast<const float4 *>(xb + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float e4[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
-        float sum = 0.f;
+    const float e4[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
+    _Float16 *hi = w.hi(sb) + (size_t)b * 256 + lane * 4, *lo = w.lo(sb) + (size_t)b * 256 + lane * 4;
+    float sum = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const _Float16 h = (_Float16)e4[j];
-            const _Float16 l = (_Float16)(e4[j] - (float)h);
-            hi[j] = h;
-            lo[j] = l;
-            sum += (float)h + (float)l;
-        }
-        // sub-block (32 columns = 8 lanes) sums, and the super-block sum
-        float sub = sum;
-        sub += __shfl_xor(sub, 1);
-        sub += __shfl_xor(sub, 2);
-        sub += __shfl_xor(sub, 4);
-        const float tot = wave_reduce_sum(sum);
-        _Float16 *xs = w.xs(sb) + (size_t)b * 16;
-        if ((lane & 7) == 0) {
-            const _Float16 h = (_Float16)sub;
-            xs[lane >> 3] = h;
-            xs[8 + (lane >> 3)] = (_Float16)(sub - (float)h);
-        }
-        if (lane == 0) w.S(sb)[b] = tot;
+    for (int j = 0; j < 4; j++) {
+        const _Float16 h = (_Float16)e4[j];
+        const _Float16 l = (_Float16)(e4[j] - (float)h);
+        hi[j] = h;
+        lo[j] = l;
+        sum += (float)h + (float)l;
+    }
+    // sub-block (32 columns = 8 lanes) sums, and the super-block sum
+    float sub = sum;
+    sub += __shfl_xor(sub, 1);
+    sub += __shfl_xor(sub, 2);
+    sub += __shfl_xor(sub, 4);
+    const float tot = wave_reduce_sum(sum);
+    _Float16 *xs = w.xs(sb) + (size_t)b * 16;
+    if ((lane & 7) == 0) {
+        const _Float16 h = (_Float16)sub;
+        xs[lane >> 3] = h;
+        xs[8 + (lane >> 3)] = (_Float16)(sub - (float)h);
+    }
+    if (lane == 0) w.SI(sb)[b] = make_float2(tot, 1.f / s);
+}
+
+// ------------------------------------------------------------------ format policies
+// Each format supplies, for one 256-column stretch ("super-block") of a row:
+//   Regs              the lane's weight bytes (row lr, K half kh), in VGPRs
+//   load(r, p, kh)    p = first byte of the row's stretch
+//   Smem / publish    per-row fp32 scales, shared through LDS
+//   compute<NT>(...)  the MFMAs and the fold into the fp32 totals
+// K-step t covers 16 columns; lane half kh supplies 8 of them.  Every weight
+// enters the MFMA as an exact fp16 integer; scales are applied in fp32.
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+struct Ctx {
+    int wave, lr, kh;
+    const _Float16 *sh_hi, *sh_lo, *sh_xs;
+    const float2 *sh_S;
+};
+constexpr int COLH = 256 + kXPad;  // halves per LDS column of the staged x slice
+
+// four byte pairs of two words -> 16-bit lanes, OR'ed into fp16 1024 + u
+__device__ __forceinline__ half8 bytes_to_h8(uint32_t w0, uint32_t w1, half2v off) {
+    const uint32_t p[4] = {__builtin_amdgcn_perm(0u, w0, 0x0C010C00u), __builtin_amdgcn_perm(0u, w0, 0x0C030C02u),
+                           __builtin_amdgcn_perm(0u, w1, 0x0C010C00u), __builtin_amdgcn_perm(0u, w1, 0x0C030C02u)};
+    half8 a;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const half2v h = __builtin_bit_cast(half2v, p[j] | 0x64006400u) - off;  // exact: small integers
+        a[2 * j] = h[0];
+        a[2 * j + 1] = h[1];
+    }
+    return a;
+}
+
+template <int NT>
+__device__ __forceinline__ void mfma_hilo(const Ctx &c, const half8 &a, int xoff, f32x16 *acc) {
+#pragma unroll
+    for (int n = 0; n < NT; n++) {
+        const int col = n * 32 + c.lr;
+        const half8 bh = *reinterpret_cast<const half8 *>(c.sh_hi + col * COLH + xoff);
+        const half8 bl = *reinterpret_cast<const half8 *>(c.sh_lo + col * COLH + xoff);
+        acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh, acc[n], 0, 0, 0);
+        acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl, acc[n], 0, 0, 0);
     }
 }
 
-// ------------------------------------------------------------------ Q4_K batched kernel
-template <int NT>  // NT = padded batch / 32
-__global__ __launch_bounds__(256) void mfma_q4k(const uint8_t *__restrict__ W, size_t pitch, int row0, int nrows,
-                                                int nsb, int ksb, XWork xw, float *__restrict__ Y, int B) {
+// tot[n][i] += s[row(i)] * acc[n][i], s = 32 per-row scales of this wave in LDS
+template <int NT>
+__device__ __forceinline__ void fold_rows(const Ctx &c, const float *s, const f32x16 *acc, f32x16 *tot) {
+#pragma unroll
+    for (int q4 = 0; q4 < 4; q4++) {
+        const float4 v = *reinterpret_cast<const float4 *>(s + q4 * 8 + 4 * c.kh);
+        const float sv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) tot[n][q4 * 4 + k] = fmaf(sv[k], acc[n][q4 * 4 + k], tot[n][q4 * 4 + k]);
+    }
+}
+
+// Q4_K (matVecQ4Kraw, LlamaTransformerHandler.java:1428-1468): w = d*ls*q - dmin*lm.
+// A = 1024 + ls*q (<= 1969, exact), built with one 24-bit multiply-add per
+// pair; 1024 * sum(x) and the min term (one more MFMA: A = [lm | lm],
+// B = [sub-block sums hi | lo]) are removed per super-block with d and dmin.
+struct FmtQ4K {
+    static constexpr int kBytes = 144;
+    static constexpr bool kSums = true;
+    struct Regs {
+        u32x4 hd;
+        u32x2 qp[4][2];
+    };
+    struct Smem {
+        float d[4][kRowsPerWave], dm[4][kRowsPerWave];
+    };
+    static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
+        r.hd = *reinterpret_cast<const u32x4 *>(p);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            r.qp[g][0] = *reinterpret_cast<const u32x2 *>(p + 16 + 32 * g + 8 * kh);
+            r.qp[g][1] = *reinterpret_cast<const u32x2 *>(p + 16 + 32 * g + 16 + 8 * kh);
+        }
+    }
+    static __device__ __forceinline__ void publish(const Regs &r, Smem &sm, const Ctx &c) {
+        if (c.kh == 0) {
+            sm.d[c.wave][c.lr] = half_bits_to_float(r.hd.x);
+            sm.dm[c.wave][c.lr] = half_bits_to_float(r.hd.x >> 16);
+        }
+    }
+    template <int NT>
+    static __device__ __forceinline__ void compute(const Regs &r, const Smem &sm, const Ctx &c, f32x16 *tot) {
+        // 6-bit scales and mins of the 8 sub-blocks (q4kScaleRaw / q4kMinRaw, :1471-1482)
+        int ls[8], lm[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            ls[j] = (int)byte_of(r.hd.y, j) & 63;
+            lm[j] = (int)byte_of(r.hd.z, j) & 63;
+            ls[j + 4] = (int)((byte_of(r.hd.w, j) & 0x0F) | ((byte_of(r.hd.y, j) & 0xC0) >> 2));
+            lm[j + 4] = (int)((byte_of(r.hd.w, j) >> 4) | ((byte_of(r.hd.z, j) & 0xC0) >> 2));
+        }
+        f32x16 acc[NT];
+#pragma unroll
+        for (int n = 0; n < NT; n++) acc[n] = (f32x16){};
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            // sub-block s = t/2: low nibbles of qs group s/2 for even s, high for odd
+            const int s = t >> 1, g = s >> 1, hiN = s & 1;
+            const u32x2 q = r.qp[g][t & 1];
+            const uint32_t nib0 = hiN ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+            const uint32_t nib1 = hiN ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+            const uint32_t pr[4] = {__builtin_amdgcn_perm(0u, nib0, 0x0C010C00u),
+                                    __builtin_amdgcn_perm(0u, nib0, 0x0C030C02u),
+                                    __builtin_amdgcn_perm(0u, nib1, 0x0C010C00u),
+                                    __builtin_amdgcn_perm(0u, nib1, 0x0C030C02u)};
+            half8 a;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t v = __umul24(pr[j], (uint32_t)ls[s]) + 0x64006400u;
+                a[2 * j] = __builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF));
+                a[2 * j + 1] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+            }
+            mfma_hilo<NT>(c, a, 16 * t + 8 * c.kh, acc);
+        }
+        half8 am;
+#pragma unroll
+        for (int j = 0; j < 8; j++) am[j] = (_Float16)lm[j];
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const int col = n * 32 + c.lr;
+            const half8 bm = *reinterpret_cast<const half8 *>(c.sh_xs + col * 16 + 8 * c.kh);
+            const f32x16 mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, (f32x16){}, 0, 0, 0);
+            const float2 si = c.sh_S[col];  // (sum of x, 1 / column scale)
+            const float S1024 = 1024.f * si.x;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+                const float4 dd = *reinterpret_cast<const float4 *>(&sm.d[c.wave][q4 * 8 + 4 * c.kh]);
+                const float4 dm = *reinterpret_cast<const float4 *>(&sm.dm[c.wave][q4 * 8 + 4 * c.kh]);
+                const float dv[4] = {dd.x, dd.y, dd.z, dd.w}, mv[4] = {dm.x, dm.y, dm.z, dm.w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int i = q4 * 4 + k;
+                    tot[n][i] = fmaf(si.y, fmaf(dv[k], acc[n][i] - S1024, -mv[k] * mn[i]), tot[n][i]);
+                }
+            }
+        }
+    }
+};
+
+// Q6_K (matVecQ6Kraw, LlamaTransformerHandler.java:1587-1638): w = (d*sc_j)*(u - 32)
+// with u = 4 bits of ql | 2 bits of qh.  A 16-column sub-block is exactly one
+// K-step, so A = u - 32 (exact) and each K-step is folded with the fp32
+// d*sc_j of its row (the reference's dN).  Step t = 8n + 2qd + j covers
+// columns 128n + 32qd + 16j .. +16 and uses scale t.
+struct FmtQ6K {
+    static constexpr int kBytes = 210;
+    static constexpr bool kSums = false;
+    struct Regs {
+        u32x2 ql[2][2][2];  // [half n][ql +32 p][j]: bytes 64n + 32p + 16j + 8kh
+        u32x2 qh[2][2];     // [n][j]: bytes 128 + 32n + 16j + 8kh
+        u32x4 sc;           // bytes 192..207
+        uint32_t dw;        // bytes 206..209: d in the high half
+    };
+    struct Smem {
+        float ds[4][16][kRowsPerWave];
+    };
+    static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                r.ql[n][0][j] = *reinterpret_cast<const u32x2a2 *>(p + 64 * n + 16 * j + 8 * kh);
+                r.ql[n][1][j] = *reinterpret_cast<const u32x2a2 *>(p + 64 * n + 32 + 16 * j + 8 * kh);
+                r.qh[n][j] = *reinterpret_cast<const u32x2a2 *>(p + 128 + 32 * n + 16 * j + 8 * kh);
+            }
+        r.sc = *reinterpret_cast<const u32x4a2 *>(p + 192);
+        r.dw = *reinterpret_cast<const u32a2 *>(p + 206);
+    }
+    static __device__ __forceinline__ void publish(const Regs &r, Smem &sm, const Ctx &c) {
+        const float d = half_bits_to_float(r.dw >> 16);
+        const uint32_t w0 = c.kh ? r.sc.z : r.sc.x, w1 = c.kh ? r.sc.w : r.sc.y;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int8_t s = (int8_t)byte_of(k < 4 ? w0 : w1, k & 3);
+            sm.ds[c.wave][8 * c.kh + k][c.lr] = d * (float)s;
+        }
+    }
+    template <int NT>
+    static __device__ __forceinline__ void compute(const Regs &r, const Smem &sm, const Ctx &c, f32x16 *tot) {
+        const half2v off = {(_Float16)1056.f, (_Float16)1056.f};  // 1024 + 32
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const int n = t >> 3, qd = (t >> 1) & 3, j = t & 1;
+            const u32x2 l = r.ql[n][qd & 1][j], h = r.qh[n][j];
+            const uint32_t u0 = ((qd >= 2 ? l.x >> 4 : l.x) & 0x0F0F0F0Fu) | (((h.x >> (2 * qd)) & 0x03030303u) << 4);
+            const uint32_t u1 = ((qd >= 2 ? l.y >> 4 : l.y) & 0x0F0F0F0Fu) | (((h.y >> (2 * qd)) & 0x03030303u) << 4);
+            const half8 a = bytes_to_h8(u0, u1, off);
+            f32x16 acc[NT];
+#pragma unroll
+            for (int m = 0; m < NT; m++) acc[m] = (f32x16){};
+            mfma_hilo<NT>(c, a, 16 * t + 8 * c.kh, acc);
+            fold_rows<NT>(c, sm.ds[c.wave][t], acc, tot);
+        }
+    }
+};
+
+// Q8_0 (matVecQ8_0raw, LlamaTransformerHandler.java:1486-1508): w = d_b * q, 8 blocks
+// of 34 B per 256 columns.  Lane half kh holds columns 16kh .. 16kh+15 of
+// block b (one 16-byte load), split over the block's two K-steps; A = q exact.
+struct FmtQ8_0 {
+    static constexpr int kBytes = 8 * 34;
+    static constexpr bool kSums = false;
+    struct Regs {
+        u32x4 q[8];     // block b: bytes 34b + 2 + 16kh .. +16
+        uint32_t d[4];  // d of blocks 4kh .. 4kh+3 (low half)
+    };
+    struct Smem {
+        float d[4][8][kRowsPerWave];
+    };
+    static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
+#pragma unroll
+        for (int b = 0; b < 8; b++) r.q[b] = *reinterpret_cast<const u32x4a2 *>(p + 34 * b + 2 + 16 * kh);
+#pragma unroll
+        for (int k = 0; k < 4; k++) r.d[k] = *reinterpret_cast<const uint16_t *>(p + 34 * (4 * kh + k));
+    }
+    static __device__ __forceinline__ void publish(const Regs &r, Smem &sm, const Ctx &c) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) sm.d[c.wave][4 * c.kh + k][c.lr] = half_bits_to_float(r.d[k]);
+    }
+    template <int NT>
+    static __device__ __forceinline__ void compute(const Regs &r, const Smem &sm, const Ctx &c, f32x16 *tot) {
+        const half2v off = {(_Float16)1152.f, (_Float16)1152.f};  // 1024 + 128
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            f32x16 acc[NT];
+#pragma unroll
+            for (int m = 0; m < NT; m++) acc[m] = (f32x16){};
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t w0 = (j ? r.q[b].z : r.q[b].x) ^ 0x80808080u;  // q + 128
+                const uint32_t w1 = (j ? r.q[b].w : r.q[b].y) ^ 0x80808080u;
+                mfma_hilo<NT>(c, bytes_to_h8(w0, w1, off), 32 * b + 16 * c.kh + 8 * j, acc);
+            }
+            fold_rows<NT>(c, sm.d[c.wave][b], acc, tot);
+        }
+    }
+};
+
+// ------------------------------------------------------------------ batched kernel
+// Q4_K applies the column's power-of-two scale inside compute (it already
+// works per column); Q6_K and Q8_0 fold per row, so their per-super-block
+// totals are scaled by the column factor here, once per super-block.
+template <class F, int NT>  // NT = padded batch / 32
+__global__ __launch_bounds__(256) void mfma_gemm(const uint8_t *__restrict__ W, size_t pitch, int row0, int nrows,
+                                                 int nsb, int ksb, XWork xw, float *__restrict__ Y, int B) {
     constexpr int BP = 32 * NT;
-    constexpr int COLH = 256 + kXPad;   // halves per LDS column
-    constexpr int XU = BP * 32 / 256;   // 16-byte x units per thread per limb
+    constexpr int XU = BP * 32 / 256;  // 16-byte x units per thread per limb
     __shared__ __align__(16) _Float16 sh_hi[BP * COLH];
     __shared__ __align__(16) _Float16 sh_lo[BP * COLH];
-    __shared__ __align__(16) _Float16 sh_xs[BP * 16];
-    __shared__ float sh_S[BP];
-    __shared__ __align__(16) float sh_d[4][kRowsPerWave], sh_dm[4][kRowsPerWave];
+    __shared__ __align__(16) _Float16 sh_xs[F::kSums ? BP * 16 : 8];
+    __shared__ float2 sh_S[BP];  // (sum of x, 1 / column scale) per column
+    __shared__ __align__(16) typename F::Smem sm;
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int kh = lane >> 5, lr = lane & 31;
+    const Ctx c{wave, lane & 31, lane >> 5, sh_hi, sh_lo, sh_xs, sh_S};
     const int rbase = blockIdx.x * kRowsPerWG + wave * kRowsPerWave;
-    const int myrow = min(rbase + lr, nrows - 1);
-    const uint8_t *rowp = W + (size_t)(row0 + myrow) * pitch;
+    const uint8_t *rowp = W + (size_t)(row0 + min(rbase + c.lr, nrows - 1)) * pitch;
     const int sb0 = blockIdx.y * ksb, sb1 = min(nsb, sb0 + ksb);
 
     // register sets for the next super-block: x slice units and weight bytes
-    u32x4 xh_n[XU], xl_n[XU], xs_n;
-    float S_n = 0.f;
-    u32x4 hd_n;
-    u32x2 qp_n[4][2];
-    // (macros rather than lambdas: the register arrays must stay in VGPRs)
+    u32x4 xh_n[XU], xl_n[XU], xs_n = {};
+    float2 S_n = make_float2(0.f, 0.f);
+    typename F::Regs w_n;
+    // (a macro rather than a lambda: the register arrays must stay in VGPRs)
 #define JH_LOAD_X(SB)                                                                                     \
     do {                                                                                                  \
         const u32x4 *hp = reinterpret_cast<const u32x4 *>(xw.hi(SB));                                    \
@@ -164,17 +395,8 @@ __global__ __launch_bounds__(256) void mfma_q4k(const uint8_t *__restrict__ W, s
             xh_n[k] = hp[threadIdx.x + 256 * k];                                                          \
             xl_n[k] = lp[threadIdx.x + 256 * k];                                                          \
         }                                                                                                 \
-        xs_n = reinterpret_cast<const u32x4 *>(xw.xs(SB))[min((int)threadIdx.x, BP * 2 - 1)];            \
-        S_n = xw.S(SB)[min((int)threadIdx.x, BP - 1)];                                                    \
-    } while (0)
-#define JH_LOAD_W(SB)                                                                                     \
-    do {                                                                                                  \
-        const uint8_t *bp = rowp + (size_t)(SB) * 144;                                                    \
-        hd_n = *reinterpret_cast<const u32x4 *>(bp);                                                      \
-        _Pragma("unroll") for (int g = 0; g < 4; g++) {                                                   \
-            qp_n[g][0] = *reinterpret_cast<const u32x2 *>(bp + 16 + 32 * g + 8 * kh);                     \
-            qp_n[g][1] = *reinterpret_cast<const u32x2 *>(bp + 16 + 32 * g + 16 + 8 * kh);                \
-        }                                                                                                 \
+        if (F::kSums) xs_n = reinterpret_cast<const u32x4 *>(xw.xs(SB))[min((int)threadIdx.x, BP * 2 - 1)]; \
+        S_n = xw.SI(SB)[min((int)threadIdx.x, BP - 1)];                                                   \
     } while (0)
 
     f32x16 tot[NT];
@@ -183,146 +405,87 @@ __global__ __launch_bounds__(256) void mfma_q4k(const uint8_t *__restrict__ W, s
 
     if (sb0 < sb1) {
         JH_LOAD_X(sb0);  // x first: waiting for it must not wait for the weight stream
-        JH_LOAD_W(sb0);
+        F::load(w_n, rowp + (size_t)sb0 * F::kBytes, c.kh);
     }
     for (int sb = sb0; sb < sb1; sb++) {
-        __syncthreads();  // the previous super-block's LDS slice is consumed
+        __syncthreads();  // the previous super-block's LDS contents are consumed
 #pragma unroll
         for (int k = 0; k < XU; k++) {
             const int i = threadIdx.x + 256 * k, col = i >> 5, u = i & 31;
             *reinterpret_cast<u32x4 *>(sh_hi + col * COLH + 8 * u) = xh_n[k];
             *reinterpret_cast<u32x4 *>(sh_lo + col * COLH + 8 * u) = xl_n[k];
         }
-        if (threadIdx.x < BP * 2) *reinterpret_cast<u32x4 *>(sh_xs + (threadIdx.x >> 1) * 16 + 8 * (threadIdx.x & 1)) = xs_n;
+        if (F::kSums && threadIdx.x < BP * 2)
+            *reinterpret_cast<u32x4 *>(sh_xs + (threadIdx.x >> 1) * 16 + 8 * (threadIdx.x & 1)) = xs_n;
         if (threadIdx.x < BP) sh_S[threadIdx.x] = S_n;
-        const u32x4 hd = hd_n;
-        u32x2 qp[4][2];
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            qp[g][0] = qp_n[g][0];
-            qp[g][1] = qp_n[g][1];
-        }
-        const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
-        if (kh == 0) {
-            sh_d[wave][lr] = d;
-            sh_dm[wave][lr] = dmin;
-        }
+        const typename F::Regs w = w_n;
+        F::publish(w, sm, c);
         if (sb + 1 < sb1) {  // prefetch the next super-block during this one's math
             JH_LOAD_X(sb + 1);
-            JH_LOAD_W(sb + 1);
+            F::load(w_n, rowp + (size_t)(sb + 1) * F::kBytes, c.kh);
         }
         __syncthreads();
-
-        // 6-bit scales and mins of the 8 sub-blocks (q4kScaleRaw / q4kMinRaw)
-        int ls[8], lm[8];
+        if constexpr (F::kSums) {
+            F::template compute<NT>(w, sm, c, tot);
+        } else {
+            f32x16 part[NT];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            ls[j] = (int)byte_of(hd.y, j) & 63;
-            lm[j] = (int)byte_of(hd.z, j) & 63;
-            ls[j + 4] = (int)((byte_of(hd.w, j) & 0x0F) | ((byte_of(hd.y, j) & 0xC0) >> 2));
-            lm[j + 4] = (int)((byte_of(hd.w, j) >> 4) | ((byte_of(hd.z, j) & 0xC0) >> 2));
-        }
-
-        f32x16 acc[NT];
-#pragma unroll
-        for (int n = 0; n < NT; n++) acc[n] = (f32x16){};
-#pragma unroll
-        for (int t = 0; t < 16; t++) {
-            // K-step t covers sub-block s = t/2, elements 16*(t&1) + 8*kh .. +8
-            const int s = t >> 1, g = s >> 1, hiN = s & 1;
-            const u32x2 q = qp[g][t & 1];
-            const uint32_t nib0 = hiN ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
-            const uint32_t nib1 = hiN ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
-            // pairs (e0,e1),(e2,e3),... as 16-bit lanes; then 0x6400 + ls*q per lane
-            uint32_t pr[4];
-            pr[0] = __builtin_amdgcn_perm(0u, nib0, 0x0C010C00u);  // e0 | e1 << 16
-            pr[1] = __builtin_amdgcn_perm(0u, nib0, 0x0C030C02u);
-            pr[2] = __builtin_amdgcn_perm(0u, nib1, 0x0C010C00u);
-            pr[3] = __builtin_amdgcn_perm(0u, nib1, 0x0C030C02u);
-            half8 a;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t v = __umul24(pr[j], (uint32_t)ls[s]) + 0x64006400u;
-                a[2 * j] = __builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF));
-                a[2 * j + 1] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
-            }
+            for (int n = 0; n < NT; n++) part[n] = (f32x16){};
+            F::template compute<NT>(w, sm, c, part);
 #pragma unroll
             for (int n = 0; n < NT; n++) {
-                const int col = n * 32 + lr;
-                const half8 bh = *reinterpret_cast<const half8 *>(sh_hi + col * COLH + 16 * t + 8 * kh);
-                const half8 bl = *reinterpret_cast<const half8 *>(sh_lo + col * COLH + 16 * t + 8 * kh);
-                acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh, acc[n], 0, 0, 0);
-                acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl, acc[n], 0, 0, 0);
-            }
-        }
-        // min term: sum_s lm_s * xsum_s, with [lm | lm] x [xsum_hi ; xsum_lo]
-        half8 am;
+                const float cs = sh_S[n * 32 + c.lr].y;
 #pragma unroll
-        for (int j = 0; j < 8; j++) am[j] = (_Float16)lm[j];
-#pragma unroll
-        for (int n = 0; n < NT; n++) {
-            const int col = n * 32 + lr;
-            const half8 bm = *reinterpret_cast<const half8 *>(sh_xs + col * 16 + 8 * kh);
-            const f32x16 mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, (f32x16){}, 0, 0, 0);
-            const float S1024 = 1024.f * sh_S[col];
-#pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-                const float4 dd = *reinterpret_cast<const float4 *>(&sh_d[wave][q4 * 8 + 4 * kh]);
-                const float4 dm = *reinterpret_cast<const float4 *>(&sh_dm[wave][q4 * 8 + 4 * kh]);
-                const float dv[4] = {dd.x, dd.y, dd.z, dd.w}, mv[4] = {dm.x, dm.y, dm.z, dm.w};
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int i = q4 * 4 + k;
-                    tot[n][i] = fmaf(dv[k], acc[n][i] - S1024, fmaf(-mv[k], mn[i], tot[n][i]));
-                }
+                for (int i = 0; i < 16; i++) tot[n][i] = fmaf(cs, part[n][i], tot[n][i]);
             }
         }
     }
-
 #undef JH_LOAD_X
-#undef JH_LOAD_W
 
-    // results, scaled back by the column's power of two
-    const int ksplit = gridDim.y;
-    if (ksplit == 1) {
-#pragma unroll
-        for (int n = 0; n < NT; n++) {
-            const int col = n * 32 + lr;
-            if (col >= B) continue;
-            const float cs = xw.scale()[col];
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int r = rbase + (i >> 2) * 8 + 4 * kh + (i & 3);
-                if (r < nrows) Y[(size_t)col * nrows + r] = tot[n][i] * cs;
-            }
-        }
-        return;
-    }
-    // split K: each split writes its partial tile; reduce_splits adds them in
-    // split order (deterministic).  A cross-workgroup hand-off inside this
-    // kernel would need a device-scope release per workgroup, which on a
-    // multi-XCD part writes back the whole L2 each time (~100 us measured).
-    float *part = xw.part() + (size_t)blockIdx.y * B * nrows;
+    // a single split writes y; otherwise each split writes its partial tile
+    // and reduce_splits adds them in split order (deterministic).  A hand-off
+    // between workgroups inside this kernel would need a device-scope release
+    // per workgroup, which on a multi-XCD part writes back the whole L2 each
+    // time (~100 us measured).
+    float *out = gridDim.y == 1 ? Y : xw.part() + (size_t)blockIdx.y * B * nrows;
 #pragma unroll
     for (int n = 0; n < NT; n++) {
-        const int col = n * 32 + lr;
+        const int col = n * 32 + c.lr;
         if (col >= B) continue;
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = rbase + (i >> 2) * 8 + 4 * kh + (i & 3);
-            if (r < nrows) part[(size_t)col * nrows + r] = tot[n][i];
+            const int r = rbase + (i >> 2) * 8 + 4 * c.kh + (i & 3);
+            if (r < nrows) out[(size_t)col * nrows + r] = tot[n][i];
         }
     }
 }
 
-// y[c][r] = scale[c] * sum over splits k (in order) of part[k][c][r]
-__global__ __launch_bounds__(256) void reduce_splits(XWork xw, int B, int nrows, int ksplit, float *__restrict__ Y) {
-    const size_t n = (size_t)B * nrows;
-    const float *p = xw.part();
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-        float v = 0.f;
-        for (int k = 0; k < ksplit; k++) v += p[(size_t)k * n + i];
-        Y[i] = v * xw.scale()[i / nrows];
+// y[i] = sum over splits k (in order) of part[k][i]; V outputs per thread
+template <typename T>
+__device__ __forceinline__ void add_to(T &a, const T &b) { a += b; }
+template <>
+__device__ __forceinline__ void add_to<float4>(float4 &a, const float4 &b) {
+    a.x += b.x;
+    a.y += b.y;
+    a.z += b.z;
+    a.w += b.w;
+}
+template <typename T>
+__global__ __launch_bounds__(256) void reduce_splits(XWork xw, int n, int ksplit, float *__restrict__ Y) {
+    const T *p = reinterpret_cast<const T *>(xw.part());
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        T v[16];
+        T acc{};
+        for (int k0 = 0; k0 < ksplit; k0 += 16) {
+            const int nk = min(16, ksplit - k0);
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (k < nk) v[k] = p[(size_t)(k0 + k) * n + i];
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (k < nk) add_to(acc, v[k]);
+        }
+        reinterpret_cast<T *>(Y)[i] = acc;
     }
 }
 
@@ -338,7 +501,7 @@ static void mfma_split(int nrows, int nsb, int &tiles, int &ksplit, int &ksb) {
 }
 
 size_t mfma_workspace_bytes(int type, int B, int cols, int rows) {
-    if (type != 12 || B < 16 || B > 64 || cols % 256 || rows < 1) return 0;
+    if ((type != 12 && type != 14 && type != 8) || B < 16 || B > 64 || cols % 256 || rows < 1) return 0;
     int tiles, ksplit, ksb;
     mfma_split(rows, cols / 256, tiles, ksplit, ksb);
     XWork w{(B + 31) / 32 * 32, cols, cols / 256, rows, ksplit, nullptr};
@@ -346,25 +509,34 @@ size_t mfma_workspace_bytes(int type, int B, int cols, int rows) {
 }
 
 hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s) {
-    if (a.type != 12 || a.batch < 16 || a.batch > 64 || a.cols % 256) return hipErrorNotSupported;
+    if ((a.type != 12 && a.type != 14 && a.type != 8) || a.batch < 16 || a.batch > 64 || a.cols % 256)
+        return hipErrorNotSupported;
     const int B = a.batch, Bp = (B + 31) / 32 * 32;
     const int nrows = a.row_end - a.row_start;
     const int nsb = a.cols / 256;
     int tiles, ksplit, ksb;
     mfma_split(nrows, nsb, tiles, ksplit, ksb);
     XWork w{Bp, a.cols, nsb, nrows, ksplit, reinterpret_cast<uint8_t *>(workspace)};
-    x_prep_mfma<<<Bp, 256, 0, s>>>(a.x, B, w);
+    x_prep_mfma<<<dim3(Bp / 4, nsb), 256, 0, s>>>(a.x, B, w);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     dim3 grid(tiles, ksplit);
-    if (Bp == 32)
-        mfma_q4k<1><<<grid, 256, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B);
-    else
-        mfma_q4k<2><<<grid, 256, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B);
+#define JH_GEMM(F, NT) mfma_gemm<F, NT><<<grid, 256, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B)
+    if (a.type == 12) {
+        if (Bp == 32) JH_GEMM(FmtQ4K, 1); else JH_GEMM(FmtQ4K, 2);
+    } else if (a.type == 14) {
+        if (Bp == 32) JH_GEMM(FmtQ6K, 1); else JH_GEMM(FmtQ6K, 2);
+    } else {
+        if (Bp == 32) JH_GEMM(FmtQ8_0, 1); else JH_GEMM(FmtQ8_0, 2);
+    }
+#undef JH_GEMM
     e = hipGetLastError();
     if (e != hipSuccess || ksplit == 1) return e;
-    const size_t n = (size_t)B * nrows;
-    reduce_splits<<<(unsigned)std::min<size_t>((n + 255) / 256, 2048), 256, 0, s>>>(w, B, nrows, ksplit, a.y);
+    const int n = B * nrows;
+    if (n % 4 == 0 && reinterpret_cast<uintptr_t>(a.y) % 16 == 0)
+        reduce_splits<float4><<<(unsigned)std::min((n / 4 + 255) / 256, 2048), 256, 0, s>>>(w, n / 4, ksplit, a.y);
+    else
+        reduce_splits<float><<<(unsigned)std::min((n + 255) / 256, 2048), 256, 0, s>>>(w, n, ksplit, a.y);
     return hipGetLastError();
 }
 

@@ -249,21 +249,48 @@ def test_batched_vs_independent(be, qtype, B):
     assert rel_err(y1, Y[-1].astype(np.float64), deq, X[-1]).max() <= TOL
 
 
-def test_batched_mfma_8b_shapes(be):
-    """The MFMA path at Llama-3-8B shapes (gate 14336x4096: no K split; k 1024x4096:
-    K split with atomics), B in {16, 32, 64}, against the oracle per column."""
-    for rows, cols in [(14336, 4096), (1024, 4096)]:
-        raw = O.quantize(O.Q4_K, weights(rows * cols, 400 + rows))
-        deq = O.dequantize(O.Q4_K, raw, rows, cols)
-        with upload(be, O.Q4_K, raw, rows, cols) as dev:
-            for B in (16, 32, 64):
-                say("mfma", rows, cols, B)
-                X = vec(cols, 500 + B, batch=B)
-                X[:, ::131] *= 30.0
-                Y = be.sgemv_batched(dev, X)
-                for j in (0, B // 2, B - 1):
-                    ref = O.matvec(O.Q4_K, raw, X[j], 0, rows, cols).astype(np.float64)
-                    assert rel_err(Y[j], ref, deq, X[j]).max() <= TOL, (rows, B, j)
+MFMA_SHAPES = [
+    (O.Q4_K, 14336, 4096),   # 8B gate/up: one K split per 4 super-blocks
+    (O.Q4_K, 1024, 4096),    # 8B k/v: K split 16 ways
+    (O.Q6_K, 4096, 14336),   # 8B ffn_down (Q4_K_M)
+    (O.Q6_K, 1024, 4096),    # 8B attn_v (Q4_K_M)
+    (O.Q8_0, 9216, 3072),    # Phi-3 fused QKV
+    (O.Q8_0, 3072, 8192),    # Phi-3 down
+]
+
+
+@pytest.mark.parametrize("qtype,rows,cols", MFMA_SHAPES)
+def test_batched_mfma_8b_shapes(be, qtype, rows, cols):
+    """The MFMA path at the 8B / Phi-3 shapes, B in {16, 32, 64}, against the
+    oracle per column (weights with 1 % outliers at 10x, x with spikes)."""
+    raw = O.quantize(qtype, weights(rows * cols, 400 + rows + qtype, outliers=True))
+    deq = O.dequantize(qtype, raw, rows, cols)
+    with upload(be, qtype, raw, rows, cols) as dev:
+        for B in (16, 32, 64):
+            say("mfma", qtype, rows, cols, B)
+            X = vec(cols, 500 + B, batch=B)
+            X[:, ::131] *= 30.0
+            Y = be.sgemv_batched(dev, X)
+            for j in (0, B // 2, B - 1):
+                ref = O.matvec(qtype, raw, X[j], 0, rows, cols).astype(np.float64)
+                assert rel_err(Y[j], ref, deq, X[j]).max() <= TOL, (rows, B, j)
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.Q8_0])
+def test_batched_mfma_odd_pitch_row_range(be, qtype):
+    """Rows whose blocks start at 2 (mod 4) bytes (Q6_K / Q8_0 with 3 super-blocks
+    per row), a row range that starts mid-tile, and a batch that is not a multiple of 32."""
+    rows, cols, B = 333, 768, 20
+    raw = O.quantize(qtype, weights(rows * cols, 80 + qtype))
+    deq = O.dequantize(qtype, raw, rows, cols)
+    X = vec(cols, 81, batch=B)
+    with upload(be, qtype, raw, rows, cols) as dev:
+        for a, b in [(0, rows), (37, 300)]:
+            say("mfma-range", qtype, a, b)
+            Y = be.sgemv_batched(dev, X, a, b)
+            for j in range(B):
+                ref = O.matvec(qtype, raw, X[j], a, b, cols).astype(np.float64)
+                assert rel_err(Y[j], ref, deq[a:b], X[j]).max() <= TOL, (a, b, j)
 
 
 def test_batched_row_range(be):
