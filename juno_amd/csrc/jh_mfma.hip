@@ -1,31 +1,33 @@
-// jh_mfma.hip -- batched decode (16 <= B <= 64) on Q4_K through LDS + fp16 MFMA.
+// jh_mfma.hip -- batched decode (16 <= B <= 64) on Q4_K / Q6_K / Q8_0 through
+// LDS + fp16 MFMA.
 //
 // Y[b][r] = sum_c deq(W[r][c]) * X[b][c] is a dense contraction once B >= 16:
-// per HBM byte it needs 2B/0.5625 flops, more than the VALU can issue without
-// packed fp32, but far below the MFMA ridge (~312 flop/B).  The kernel keeps
-// the weights exact and moves the arithmetic to v_mfma_f32_32x32x16_f16:
+// per HBM byte it needs 2B/0.5625 flops (Q4_K), more than the VALU can issue
+// without packed fp32, but below the MFMA ridge (~312 flop/B).  The kernels
+// keep every weight integer exact and move the arithmetic to
+// v_mfma_f32_32x32x16_f16 with x as the A operand and weights as B, so the
+// accumulator of a lane holds one weight row (its own) for 16 batch columns:
 //
-//  * A (weights): for Q4_K, w = d*ls*q - dmin*lm with 6-bit ls and 4-bit q, so
-//    ls*q <= 945 is an exact fp16 integer.  Each lane builds its A fragment as
-//    the fp16 bit pattern 0x6400 | ls*q, i.e. 1024 + ls*q, with one integer
-//    multiply-add per pair; the 1024 offset is removed after the super-block
-//    as 1024 * sum(x).  The per-row d and dmin are applied in fp32 once per
-//    256-column super-block (fresh accumulators per super-block).
-//  * The min term dmin * sum_s lm_s * sum(x over sub-block s) is one more
-//    MFMA per super-block: A = [lm_0..7 | lm_0..7], B = [xsum_hi | xsum_lo].
-//  * B (activations): x is split into fp16 hi + lo limbs (x = hi + lo to
-//    ~2^-22; one fp16 rounding of x alone would exceed the 1e-3 bar), after a
-//    per-column power-of-two scaling that keeps fp16 in range.  A small prep
-//    kernel writes hi, lo, sub-block sums and super-block sums once per call
-//    into a workspace; workgroups stage each super-block's slice in LDS.
-//  * Work split: a workgroup is 4 waves x 32 rows = 128 rows, all B columns,
-//    and a range of super-blocks.  Every x fragment staged in LDS feeds 128
-//    rows (operand traffic ~3.5x the weight bytes at B = 32, within LDS
-//    bandwidth).  The next super-block's weights and x slice are loaded while
-//    the current one is multiplied.  When the row tiles are too few to fill
-//    256 CUs the K range is split across workgroups; each split writes its
-//    partial tile to the workspace and a small kernel adds the partials in
-//    split order (deterministic; no float atomics).
+//  * Weights: each format turns its packed integers into exact fp16 integers
+//    (Q4_K: 1024 + ls*q <= 1969 by one 24-bit multiply-add per pair; Q6_K:
+//    u - 32; Q8_0: q) and applies its fp32 scales per row in registers -- Q4_K
+//    once per 256 columns with d and dmin (the min term is one extra MFMA
+//    against per-sub-block sums of x), Q6_K per 16-column sub-block with the
+//    reference's d*sc, Q8_0 per 32-column block with d.
+//  * Activations: x is split into fp16 hi + lo limbs (x = hi + lo to ~2^-22,
+//    so only the order of summation differs from fp32) after a power-of-two
+//    scale per (column, 256-column super-block) that keeps fp16 in range.  A
+//    prep kernel writes the limbs, sub-block sums and scales once per call,
+//    super-block major, into a workspace.
+//  * Work split: a workgroup is kWaves waves x 32 rows, all B columns, and a
+//    range of super-blocks.  Per super-block it stages the x slice in LDS
+//    (shared by all its rows) and each wave stages its rows' packed blocks in
+//    a wave-private LDS window with aligned, coalesced 16-byte loads; the
+//    next super-block's loads are in flight during the current one's math.
+//    When the row tiles are too few to fill the GPU the K range is split
+//    across workgroups; each split writes its partial tile to the workspace
+//    and a small kernel adds the partials in split order (deterministic; no
+//    float atomics).
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
 
@@ -40,10 +42,13 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2a2 __attribute__((ext_vector_type(2), aligned(2)));
 typedef uint32_t u32x4a2 __attribute__((ext_vector_type(4), aligned(2)));
 typedef uint32_t u32a2 __attribute__((aligned(2)));
-constexpr int kMinWorkgroups = 512;  // split K until the grid has this many
+constexpr int kPrefetch = 1;  // super-blocks of weight chunks in flight per wave (B <= 32)
+constexpr int kMinWorkgroups = 256;  // split K until the grid has this many
 
 constexpr int kRowsPerWave = 32;
-constexpr int kRowsPerWG = 4 * kRowsPerWave;
+constexpr int kWaves = 8;  // waves per workgroup: 256 rows share each staged x slice
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRowsPerWG = kWaves * kRowsPerWave;
 constexpr int kXPad = 8;  // halves of padding per LDS column (spreads banks)
 
 // ------------------------------------------------------------------ workspace layout
@@ -134,6 +139,14 @@ struct Ctx {
 };
 constexpr int COLH = 256 + kXPad;  // halves per LDS column of the staged x slice
 
+// Operand roles: x is the A operand (its 32 rows are batch columns) and the
+// weights are B, so D[b][r] = sum_k x[b][k] w[r][k].  In the 32x32x16 layout
+// lane (lr, kh) supplies weight row lr (K elements 8kh .. 8kh+7) and holds
+// D for row lr and batch columns 8(i/4) + 4kh + (i%4), i < 16: every per-row
+// scale (d, dmin, d*sc) lives in the lane's own registers, and consecutive
+// lanes store consecutive rows.
+__device__ __forceinline__ int batch_of(int n, int i, int kh) { return n * 32 + 8 * (i >> 2) + 4 * kh + (i & 3); }
+
 // four byte pairs of two words -> 16-bit lanes, OR'ed into fp16 1024 + u
 __device__ __forceinline__ half8 bytes_to_h8(uint32_t w0, uint32_t w1, half2v off) {
     const uint32_t p[4] = {__builtin_amdgcn_perm(0u, w0, 0x0C010C00u), __builtin_amdgcn_perm(0u, w0, 0x0C030C02u),
@@ -148,45 +161,45 @@ __device__ __forceinline__ half8 bytes_to_h8(uint32_t w0, uint32_t w1, half2v of
     return a;
 }
 
+// acc[n] += x_hi . w + x_lo . w over one K-step (x columns at xoff)
 template <int NT>
-__device__ __forceinline__ void mfma_hilo(const Ctx &c, const half8 &a, int xoff, f32x16 *acc) {
+__device__ __forceinline__ void mfma_xw(const Ctx &c, const half8 &w, int xoff, f32x16 *acc) {
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const int col = n * 32 + c.lr;
-        const half8 bh = *reinterpret_cast<const half8 *>(c.sh_hi + col * COLH + xoff);
-        const half8 bl = *reinterpret_cast<const half8 *>(c.sh_lo + col * COLH + xoff);
-        acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh, acc[n], 0, 0, 0);
-        acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl, acc[n], 0, 0, 0);
+        const half8 xh = *reinterpret_cast<const half8 *>(c.sh_hi + col * COLH + xoff);
+        const half8 xl = *reinterpret_cast<const half8 *>(c.sh_lo + col * COLH + xoff);
+        acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, w, acc[n], 0, 0, 0);
+        acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, w, acc[n], 0, 0, 0);
     }
 }
 
-// tot[n][i] += s[row(i)] * acc[n][i], s = 32 per-row scales of this wave in LDS
+// (S, 1/scale) of the 16 batch columns a lane holds for tile n
 template <int NT>
-__device__ __forceinline__ void fold_rows(const Ctx &c, const float *s, const f32x16 *acc, f32x16 *tot) {
+__device__ __forceinline__ void col_terms(const Ctx &c, int n, float (&S)[16], float (&cs)[16]) {
 #pragma unroll
-    for (int q4 = 0; q4 < 4; q4++) {
-        const float4 v = *reinterpret_cast<const float4 *>(s + q4 * 8 + 4 * c.kh);
-        const float sv[4] = {v.x, v.y, v.z, v.w};
+    for (int q = 0; q < 4; q++)
 #pragma unroll
-        for (int n = 0; n < NT; n++)
-#pragma unroll
-            for (int k = 0; k < 4; k++) tot[n][q4 * 4 + k] = fmaf(sv[k], acc[n][q4 * 4 + k], tot[n][q4 * 4 + k]);
-    }
+        for (int h = 0; h < 2; h++) {
+            const float4 v = *reinterpret_cast<const float4 *>(c.sh_S + n * 32 + 8 * q + 4 * c.kh + 2 * h);
+            S[4 * q + 2 * h] = v.x;
+            cs[4 * q + 2 * h] = v.y;
+            S[4 * q + 2 * h + 1] = v.z;
+            cs[4 * q + 2 * h + 1] = v.w;
+        }
 }
 
 // Q4_K (matVecQ4Kraw, LlamaTransformerHandler.java:1428-1468): w = d*ls*q - dmin*lm.
-// A = 1024 + ls*q (<= 1969, exact), built with one 24-bit multiply-add per
-// pair; 1024 * sum(x) and the min term (one more MFMA: A = [lm | lm],
-// B = [sub-block sums hi | lo]) are removed per super-block with d and dmin.
+// B = 1024 + ls*q (<= 1969, exact), built with one 24-bit multiply-add per
+// pair; 1024 * sum(x) and the min term (one more MFMA: A = [sub-block sums
+// hi | lo], B = [lm | lm]) are removed per super-block with d and dmin.
 struct FmtQ4K {
     static constexpr int kBytes = 144;
+    static constexpr int kChunks = 9;  // rows are 16-byte aligned (pitch 144 * n, aligned base)
     static constexpr bool kSums = true;
     struct Regs {
         u32x4 hd;
         u32x2 qp[4][2];
-    };
-    struct Smem {
-        float d[4][kRowsPerWave], dm[4][kRowsPerWave];
     };
     static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
         r.hd = *reinterpret_cast<const u32x4 *>(p);
@@ -196,14 +209,8 @@ struct FmtQ4K {
             r.qp[g][1] = *reinterpret_cast<const u32x2 *>(p + 16 + 32 * g + 16 + 8 * kh);
         }
     }
-    static __device__ __forceinline__ void publish(const Regs &r, Smem &sm, const Ctx &c) {
-        if (c.kh == 0) {
-            sm.d[c.wave][c.lr] = half_bits_to_float(r.hd.x);
-            sm.dm[c.wave][c.lr] = half_bits_to_float(r.hd.x >> 16);
-        }
-    }
     template <int NT>
-    static __device__ __forceinline__ void compute(const Regs &r, const Smem &sm, const Ctx &c, f32x16 *tot) {
+    static __device__ __forceinline__ void compute(const Regs &r, const Ctx &c, f32x16 *tot) {
         // 6-bit scales and mins of the 8 sub-blocks (q4kScaleRaw / q4kMinRaw, :1471-1482)
         int ls[8], lm[8];
 #pragma unroll
@@ -227,56 +234,47 @@ struct FmtQ4K {
                                     __builtin_amdgcn_perm(0u, nib0, 0x0C030C02u),
                                     __builtin_amdgcn_perm(0u, nib1, 0x0C010C00u),
                                     __builtin_amdgcn_perm(0u, nib1, 0x0C030C02u)};
-            half8 a;
+            half8 w;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const uint32_t v = __umul24(pr[j], (uint32_t)ls[s]) + 0x64006400u;
-                a[2 * j] = __builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF));
-                a[2 * j + 1] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+                w[2 * j] = __builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF));
+                w[2 * j + 1] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
             }
-            mfma_hilo<NT>(c, a, 16 * t + 8 * c.kh, acc);
+            mfma_xw<NT>(c, w, 16 * t + 8 * c.kh, acc);
         }
-        half8 am;
+        half8 wm;
 #pragma unroll
-        for (int j = 0; j < 8; j++) am[j] = (_Float16)lm[j];
+        for (int j = 0; j < 8; j++) wm[j] = (_Float16)lm[j];
+        const float d = half_bits_to_float(r.hd.x), dmin = half_bits_to_float(r.hd.x >> 16);
 #pragma unroll
         for (int n = 0; n < NT; n++) {
             const int col = n * 32 + c.lr;
-            const half8 bm = *reinterpret_cast<const half8 *>(c.sh_xs + col * 16 + 8 * c.kh);
-            const f32x16 mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, (f32x16){}, 0, 0, 0);
-            const float2 si = c.sh_S[col];  // (sum of x, 1 / column scale)
-            const float S1024 = 1024.f * si.x;
+            const half8 xm = *reinterpret_cast<const half8 *>(c.sh_xs + col * 16 + 8 * c.kh);
+            const f32x16 mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(xm, wm, (f32x16){}, 0, 0, 0);
+            float S[16], cs[16];
+            col_terms<NT>(c, n, S, cs);
 #pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-                const float4 dd = *reinterpret_cast<const float4 *>(&sm.d[c.wave][q4 * 8 + 4 * c.kh]);
-                const float4 dm = *reinterpret_cast<const float4 *>(&sm.dm[c.wave][q4 * 8 + 4 * c.kh]);
-                const float dv[4] = {dd.x, dd.y, dd.z, dd.w}, mv[4] = {dm.x, dm.y, dm.z, dm.w};
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const int i = q4 * 4 + k;
-                    tot[n][i] = fmaf(si.y, fmaf(dv[k], acc[n][i] - S1024, -mv[k] * mn[i]), tot[n][i]);
-                }
-            }
+            for (int i = 0; i < 16; i++)
+                tot[n][i] = fmaf(cs[i], fmaf(d, fmaf(-1024.f, S[i], acc[n][i]), -dmin * mn[i]), tot[n][i]);
         }
     }
 };
 
 // Q6_K (matVecQ6Kraw, LlamaTransformerHandler.java:1587-1638): w = (d*sc_j)*(u - 32)
 // with u = 4 bits of ql | 2 bits of qh.  A 16-column sub-block is exactly one
-// K-step, so A = u - 32 (exact) and each K-step is folded with the fp32
-// d*sc_j of its row (the reference's dN).  Step t = 8n + 2qd + j covers
-// columns 128n + 32qd + 16j .. +16 and uses scale t.
+// K-step, so B = u - 32 (exact) and each K-step is folded with the fp32
+// d*sc_j of the lane's row (the reference's dN).  Step t = 8n + 2qd + j
+// covers columns 128n + 32qd + 16j .. +16 and uses scale t.
 struct FmtQ6K {
     static constexpr int kBytes = 210;
+    static constexpr int kChunks = (kBytes + 14 + 15) / 16;  // a 2-byte-aligned block spans <= 14 chunks
     static constexpr bool kSums = false;
     struct Regs {
         u32x2 ql[2][2][2];  // [half n][ql +32 p][j]: bytes 64n + 32p + 16j + 8kh
         u32x2 qh[2][2];     // [n][j]: bytes 128 + 32n + 16j + 8kh
         u32x4 sc;           // bytes 192..207
         uint32_t dw;        // bytes 206..209: d in the high half
-    };
-    struct Smem {
-        float ds[4][16][kRowsPerWave];
     };
     static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
 #pragma unroll
@@ -290,59 +288,49 @@ struct FmtQ6K {
         r.sc = *reinterpret_cast<const u32x4a2 *>(p + 192);
         r.dw = *reinterpret_cast<const u32a2 *>(p + 206);
     }
-    static __device__ __forceinline__ void publish(const Regs &r, Smem &sm, const Ctx &c) {
-        const float d = half_bits_to_float(r.dw >> 16);
-        const uint32_t w0 = c.kh ? r.sc.z : r.sc.x, w1 = c.kh ? r.sc.w : r.sc.y;
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int8_t s = (int8_t)byte_of(k < 4 ? w0 : w1, k & 3);
-            sm.ds[c.wave][8 * c.kh + k][c.lr] = d * (float)s;
-        }
-    }
     template <int NT>
-    static __device__ __forceinline__ void compute(const Regs &r, const Smem &sm, const Ctx &c, f32x16 *tot) {
+    static __device__ __forceinline__ void compute(const Regs &r, const Ctx &c, f32x16 *tot) {
         const half2v off = {(_Float16)1056.f, (_Float16)1056.f};  // 1024 + 32
+        const float d = half_bits_to_float(r.dw >> 16);
 #pragma unroll
         for (int t = 0; t < 16; t++) {
             const int n = t >> 3, qd = (t >> 1) & 3, j = t & 1;
             const u32x2 l = r.ql[n][qd & 1][j], h = r.qh[n][j];
             const uint32_t u0 = ((qd >= 2 ? l.x >> 4 : l.x) & 0x0F0F0F0Fu) | (((h.x >> (2 * qd)) & 0x03030303u) << 4);
             const uint32_t u1 = ((qd >= 2 ? l.y >> 4 : l.y) & 0x0F0F0F0Fu) | (((h.y >> (2 * qd)) & 0x03030303u) << 4);
-            const half8 a = bytes_to_h8(u0, u1, off);
             f32x16 acc[NT];
 #pragma unroll
             for (int m = 0; m < NT; m++) acc[m] = (f32x16){};
-            mfma_hilo<NT>(c, a, 16 * t + 8 * c.kh, acc);
-            fold_rows<NT>(c, sm.ds[c.wave][t], acc, tot);
+            mfma_xw<NT>(c, bytes_to_h8(u0, u1, off), 16 * t + 8 * c.kh, acc);
+            const float ds = d * (float)(int8_t)byte_of(t < 4 ? r.sc.x : t < 8 ? r.sc.y : t < 12 ? r.sc.z : r.sc.w, t & 3);
+#pragma unroll
+            for (int m = 0; m < NT; m++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) tot[m][i] = fmaf(ds, acc[m][i], tot[m][i]);
         }
     }
 };
 
 // Q8_0 (matVecQ8_0raw, LlamaTransformerHandler.java:1486-1508): w = d_b * q, 8 blocks
 // of 34 B per 256 columns.  Lane half kh holds columns 16kh .. 16kh+15 of
-// block b (one 16-byte load), split over the block's two K-steps; A = q exact.
+// block b (one 16-byte load), split over the block's two K-steps; B = q exact.
 struct FmtQ8_0 {
     static constexpr int kBytes = 8 * 34;
+    static constexpr int kChunks = (kBytes + 14 + 15) / 16;
     static constexpr bool kSums = false;
     struct Regs {
         u32x4 q[8];     // block b: bytes 34b + 2 + 16kh .. +16
-        uint32_t d[4];  // d of blocks 4kh .. 4kh+3 (low half)
-    };
-    struct Smem {
-        float d[4][8][kRowsPerWave];
+        uint32_t d[8];  // d of block b (low half)
     };
     static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
 #pragma unroll
-        for (int b = 0; b < 8; b++) r.q[b] = *reinterpret_cast<const u32x4a2 *>(p + 34 * b + 2 + 16 * kh);
-#pragma unroll
-        for (int k = 0; k < 4; k++) r.d[k] = *reinterpret_cast<const uint16_t *>(p + 34 * (4 * kh + k));
-    }
-    static __device__ __forceinline__ void publish(const Regs &r, Smem &sm, const Ctx &c) {
-#pragma unroll
-        for (int k = 0; k < 4; k++) sm.d[c.wave][4 * c.kh + k][c.lr] = half_bits_to_float(r.d[k]);
+        for (int b = 0; b < 8; b++) {
+            r.q[b] = *reinterpret_cast<const u32x4a2 *>(p + 34 * b + 2 + 16 * kh);
+            r.d[b] = *reinterpret_cast<const uint16_t *>(p + 34 * b);
+        }
     }
     template <int NT>
-    static __device__ __forceinline__ void compute(const Regs &r, const Smem &sm, const Ctx &c, f32x16 *tot) {
+    static __device__ __forceinline__ void compute(const Regs &r, const Ctx &c, f32x16 *tot) {
         const half2v off = {(_Float16)1152.f, (_Float16)1152.f};  // 1024 + 128
 #pragma unroll
         for (int b = 0; b < 8; b++) {
@@ -353,111 +341,138 @@ struct FmtQ8_0 {
             for (int j = 0; j < 2; j++) {
                 const uint32_t w0 = (j ? r.q[b].z : r.q[b].x) ^ 0x80808080u;  // q + 128
                 const uint32_t w1 = (j ? r.q[b].w : r.q[b].y) ^ 0x80808080u;
-                mfma_hilo<NT>(c, bytes_to_h8(w0, w1, off), 32 * b + 16 * c.kh + 8 * j, acc);
+                mfma_xw<NT>(c, bytes_to_h8(w0, w1, off), 32 * b + 16 * c.kh + 8 * j, acc);
             }
-            fold_rows<NT>(c, sm.d[c.wave][b], acc, tot);
+            const float d = half_bits_to_float(r.d[b]);
+#pragma unroll
+            for (int m = 0; m < NT; m++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) tot[m][i] = fmaf(d, acc[m][i], tot[m][i]);
         }
     }
 };
 
 // ------------------------------------------------------------------ batched kernel
-// Q4_K applies the column's power-of-two scale inside compute (it already
-// works per column); Q6_K and Q8_0 fold per row, so their per-super-block
-// totals are scaled by the column factor here, once per super-block.
-template <class F, int NT>  // NT = padded batch / 32
-__global__ __launch_bounds__(256) void mfma_gemm(const uint8_t *__restrict__ W, size_t pitch, int row0, int nrows,
-                                                 int nsb, int ksb, XWork xw, float *__restrict__ Y, int B) {
+template <class F, int NT, int PD>  // NT = padded batch / 32, PD = weight prefetch depth (super-blocks)
+__global__ __launch_bounds__(kThreads) void mfma_gemm(const uint8_t *__restrict__ W, size_t pitch, int row0, int nrows,
+                                                      int nsb, int ksb, XWork xw, float *__restrict__ Y, int B) {
     constexpr int BP = 32 * NT;
-    constexpr int XU = BP * 32 / 256;  // 16-byte x units per thread per limb
+    constexpr int XU = BP * 32 / kThreads;  // 16-byte x units per thread per limb
+    constexpr int CH = F::kChunks;          // 16-byte chunks staged per row and super-block
+    constexpr int CL = (kRowsPerWave * CH + 63) / 64;  // chunks per lane
     __shared__ __align__(16) _Float16 sh_hi[BP * COLH];
     __shared__ __align__(16) _Float16 sh_lo[BP * COLH];
     __shared__ __align__(16) _Float16 sh_xs[F::kSums ? BP * 16 : 8];
-    __shared__ float2 sh_S[BP];  // (sum of x, 1 / column scale) per column
-    __shared__ __align__(16) typename F::Smem sm;
+    __shared__ __align__(16) float2 sh_S[BP];  // (sum of x, 1 / column scale) per column
+    __shared__ __align__(16) uint8_t sh_w[kWaves][kRowsPerWave * CH * 16];  // wave-private row blocks
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const Ctx c{wave, lane & 31, lane >> 5, sh_hi, sh_lo, sh_xs, sh_S};
     const int rbase = blockIdx.x * kRowsPerWG + wave * kRowsPerWave;
-    const uint8_t *rowp = W + (size_t)(row0 + min(rbase + c.lr, nrows - 1)) * pitch;
     const int sb0 = blockIdx.y * ksb, sb1 = min(nsb, sb0 + ksb);
+    auto row_off = [&](int rho) { return (size_t)(row0 + min(rbase + rho, nrows - 1)) * pitch; };
+    // Weight staging: chunk j = lane + 64 k of the wave's 32 x CH chunk grid is
+    // row j / CH, 16-byte piece j % CH of that row's aligned window.  Whole
+    // aligned 16-byte lanes, consecutive within a row: few cache accesses per
+    // load, instead of 8-byte gathers from 32 rows at 2-byte alignment.
+    size_t coff[CL];
+#pragma unroll
+    for (int k = 0; k < CL; k++) {
+        const int j = min(lane + 64 * k, kRowsPerWave * CH - 1);
+        coff[k] = row_off(j / CH) + 16 * (j % CH);
+    }
+    const size_t myoff = row_off(c.lr);
+    uint8_t *wslot = sh_w[wave];
 
-    // register sets for the next super-block: x slice units and weight bytes
-    u32x4 xh_n[XU], xl_n[XU], xs_n = {};
+    u32x4 xh_n[XU], xl_n[XU], xs_n = {}, ch_n[PD][CL];
     float2 S_n = make_float2(0.f, 0.f);
-    typename F::Regs w_n;
     // (a macro rather than a lambda: the register arrays must stay in VGPRs)
-#define JH_LOAD_X(SB)                                                                                     \
-    do {                                                                                                  \
-        const u32x4 *hp = reinterpret_cast<const u32x4 *>(xw.hi(SB));                                    \
-        const u32x4 *lp = reinterpret_cast<const u32x4 *>(xw.lo(SB));                                    \
-        _Pragma("unroll") for (int k = 0; k < XU; k++) {                                                  \
-            xh_n[k] = hp[threadIdx.x + 256 * k];                                                          \
-            xl_n[k] = lp[threadIdx.x + 256 * k];                                                          \
-        }                                                                                                 \
+#define JH_LOAD_W(ST, SB)                                                                                  \
+    do {                                                                                                   \
+        const size_t sbo = (size_t)(SB) * F::kBytes;                                                       \
+        _Pragma("unroll") for (int k = 0; k < CL; k++)                                                     \
+            ch_n[ST][k] = *reinterpret_cast<const u32x4 *>(W + ((coff[k] + sbo) & ~size_t(15)));           \
+    } while (0)
+#define JH_LOAD_X(SB)                                                                                      \
+    do {                                                                                                   \
+        const u32x4 *hp = reinterpret_cast<const u32x4 *>(xw.hi(SB));                                     \
+        const u32x4 *lp = reinterpret_cast<const u32x4 *>(xw.lo(SB));                                     \
+        _Pragma("unroll") for (int k = 0; k < XU; k++) {                                                   \
+            xh_n[k] = hp[threadIdx.x + kThreads * k];                                                      \
+            xl_n[k] = lp[threadIdx.x + kThreads * k];                                                      \
+        }                                                                                                  \
         if (F::kSums) xs_n = reinterpret_cast<const u32x4 *>(xw.xs(SB))[min((int)threadIdx.x, BP * 2 - 1)]; \
-        S_n = xw.SI(SB)[min((int)threadIdx.x, BP - 1)];                                                   \
+        S_n = xw.SI(SB)[min((int)threadIdx.x, BP - 1)];                                                    \
     } while (0)
 
     f32x16 tot[NT];
 #pragma unroll
     for (int n = 0; n < NT; n++) tot[n] = (f32x16){};
 
-    if (sb0 < sb1) {
-        JH_LOAD_X(sb0);  // x first: waiting for it must not wait for the weight stream
-        F::load(w_n, rowp + (size_t)sb0 * F::kBytes, c.kh);
-    }
+    if (sb0 < sb1) JH_LOAD_X(sb0);
+#pragma unroll
+    for (int st = 0; st < PD; st++)
+        if (sb0 + st < sb1) JH_LOAD_W(st, sb0 + st);
     for (int sb = sb0; sb < sb1; sb++) {
         __syncthreads();  // the previous super-block's LDS contents are consumed
 #pragma unroll
         for (int k = 0; k < XU; k++) {
-            const int i = threadIdx.x + 256 * k, col = i >> 5, u = i & 31;
+            const int i = threadIdx.x + kThreads * k, col = i >> 5, u = i & 31;
             *reinterpret_cast<u32x4 *>(sh_hi + col * COLH + 8 * u) = xh_n[k];
             *reinterpret_cast<u32x4 *>(sh_lo + col * COLH + 8 * u) = xl_n[k];
         }
         if (F::kSums && threadIdx.x < BP * 2)
             *reinterpret_cast<u32x4 *>(sh_xs + (threadIdx.x >> 1) * 16 + 8 * (threadIdx.x & 1)) = xs_n;
         if (threadIdx.x < BP) sh_S[threadIdx.x] = S_n;
-        const typename F::Regs w = w_n;
-        F::publish(w, sm, c);
-        if (sb + 1 < sb1) {  // prefetch the next super-block during this one's math
-            JH_LOAD_X(sb + 1);
-            F::load(w_n, rowp + (size_t)(sb + 1) * F::kBytes, c.kh);
-        }
+#pragma unroll
+        for (int k = 0; k < CL; k++)
+            if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot + 16 * (lane + 64 * k)) = ch_n[0][k];
+        // this lane's row block inside its staged window (same wave: no barrier)
+        typename F::Regs w;
+        F::load(w, wslot + c.lr * CH * 16 + ((myoff + (size_t)sb * F::kBytes) & 15), c.kh);
+        // the loads below overlap this super-block's math
+        if (sb + 1 < sb1) JH_LOAD_X(sb + 1);
+#pragma unroll
+        for (int st = 0; st + 1 < PD; st++)
+#pragma unroll
+            for (int k = 0; k < CL; k++) ch_n[st][k] = ch_n[st + 1][k];
+        if (sb + PD < sb1) JH_LOAD_W(PD - 1, sb + PD);
         __syncthreads();
         if constexpr (F::kSums) {
-            F::template compute<NT>(w, sm, c, tot);
+            F::template compute<NT>(w, c, tot);
         } else {
             f32x16 part[NT];
 #pragma unroll
             for (int n = 0; n < NT; n++) part[n] = (f32x16){};
-            F::template compute<NT>(w, sm, c, part);
+            F::template compute<NT>(w, c, part);
 #pragma unroll
             for (int n = 0; n < NT; n++) {
-                const float cs = sh_S[n * 32 + c.lr].y;
+                float S[16], cs[16];
+                col_terms<NT>(c, n, S, cs);
 #pragma unroll
-                for (int i = 0; i < 16; i++) tot[n][i] = fmaf(cs, part[n][i], tot[n][i]);
+                for (int i = 0; i < 16; i++) tot[n][i] = fmaf(cs[i], part[n][i], tot[n][i]);
             }
         }
     }
 #undef JH_LOAD_X
+#undef JH_LOAD_W
 
     // a single split writes y; otherwise each split writes its partial tile
     // and reduce_splits adds them in split order (deterministic).  A hand-off
     // between workgroups inside this kernel would need a device-scope release
     // per workgroup, which on a multi-XCD part writes back the whole L2 each
     // time (~100 us measured).
+    const int r = rbase + c.lr;
+    if (r >= nrows) return;
     float *out = gridDim.y == 1 ? Y : xw.part() + (size_t)blockIdx.y * B * nrows;
 #pragma unroll
-    for (int n = 0; n < NT; n++) {
-        const int col = n * 32 + c.lr;
-        if (col >= B) continue;
+    for (int n = 0; n < NT; n++)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = rbase + (i >> 2) * 8 + 4 * c.kh + (i & 3);
-            if (r < nrows) out[(size_t)col * nrows + r] = tot[n][i];
+            const int b = batch_of(n, i, c.kh);
+            if (b < B) out[(size_t)b * nrows + r] = tot[n][i];
         }
-    }
 }
 
 // y[i] = sum over splits k (in order) of part[k][i]; V outputs per thread
@@ -511,6 +526,8 @@ size_t mfma_workspace_bytes(int type, int B, int cols, int rows) {
 hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s) {
     if ((a.type != 12 && a.type != 14 && a.type != 8) || a.batch < 16 || a.batch > 64 || a.cols % 256)
         return hipErrorNotSupported;
+    if (a.type == 12 && ((reinterpret_cast<uintptr_t>(a.w) | a.pitch) & 15))
+        return hipErrorNotSupported;  // Q4_K rows are staged as whole aligned 16-byte chunks
     const int B = a.batch, Bp = (B + 31) / 32 * 32;
     const int nrows = a.row_end - a.row_start;
     const int nsb = a.cols / 256;
@@ -521,7 +538,7 @@ hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     dim3 grid(tiles, ksplit);
-#define JH_GEMM(F, NT) mfma_gemm<F, NT><<<grid, 256, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B)
+#define JH_GEMM(F, NT) mfma_gemm<F, NT, NT == 1 ? kPrefetch : 1><<<grid, kThreads, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B)
     if (a.type == 12) {
         if (Bp == 32) JH_GEMM(FmtQ4K, 1); else JH_GEMM(FmtQ4K, 2);
     } else if (a.type == 14) {
