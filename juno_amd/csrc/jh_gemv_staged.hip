@@ -18,14 +18,18 @@
 //    This needs ~1.7 VALU instructions per Q4_K weight instead of ~2.8 for an
 //    fp32 convert+FMA path, which would otherwise bound the kernel below the
 //    HBM roofline.  Block scales (d, dmin, 6-bit / int8 sub-scales) are fp32.
-//  * Persistent workgroups.  x is prepared once per workgroup and kept in
-//    registers while the workgroup walks many row groups.
+//  * Persistent workgroups.  x is converted once per workgroup and kept in
+//    registers while the workgroup walks many row groups: with one column
+//    tile the waves share one LDS image of all of x; with 2-4 column tiles
+//    each lane converts just its own columns straight into registers (no
+//    image, no barrier before the walk).
 //  * Wide rows (more than 16 super-blocks, or 64 Q8_0 blocks) are split into
 //    column tiles over 2 or 4 waves of a workgroup; the partial sums meet in LDS.
 //
 // Numerics: weights are used exactly; the only approximation beyond fp32
-// summation order is rounding x to 24 bits of its 256-column block maximum
-// (error <= 2^-24 * max|x| per element), the size of an fp32 rounding.
+// summation order is rounding x to 24 bits of the maximum over its 256-column
+// block (shared image) or the lane's 64 (Q8_0: 32) columns (error <= 2^-24 *
+// that maximum per element), the size of an fp32 rounding.
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
 
@@ -95,14 +99,50 @@ __device__ __forceinline__ uint32_t lds_word(const uint32_t *w, uint32_t sh, int
 
 // --------------------------------------------------------------------------- x preparation
 //
-// Every x element becomes a 24-bit integer xi = rint(x / a) with one scale
-// a = max|x| / (2^23 - 1) per 256 columns, split into three byte limbs
+// Every x element a lane needs becomes a 24-bit integer xi = rint(x / a) with
+// one scale a = max|x| / (2^23 - 1) over a group of columns (the lane's own 64
+// for Q4_K / Q6_K or 32 for Q8_0; a 256-column block in the shared image
+// below), split into three byte limbs
 //   xi = 65536 * hi + 256 * mid + lo,   hi signed, mid and lo unsigned,
 // so that sum(q * x) = a * (65536 * sum(q*hi) + 256 * sum(q*mid) + sum(q*lo))
 // with three v_dot4 products per 4 quants and exact integer sums.  The
-// resolution is 2^-23 of the block maximum (about fp32's), so the integer
+// resolution is 2^-23 of the group's maximum (about fp32's), so the integer
 // path adds no error of consequence to the fp32 accumulation.
-//
+
+// cols is a multiple of 32: a float4 is either wholly inside or wholly past
+// the end.  The load is clamped in range; to_limbs zeroes the float4s that
+// lie past the end (at use, so the load is not waited for here).
+__device__ __forceinline__ float4 x_load4(const float *X, int cols, int c) {
+    return *reinterpret_cast<const float4 *>(X + min(c, cols - 4));
+}
+__device__ __forceinline__ float4 x_mask4(float4 v, int cols, int c) {
+    return c < cols ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+__device__ __forceinline__ float amax4(float4 v) {
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+constexpr float kMaxInt = 8388607.f;  // 2^23 - 1
+
+// the three limb dwords of 4 consecutive x values (inv = (2^23 - 1) / max)
+__device__ __forceinline__ void to_limbs(float4 v, float inv, uint32_t &h, uint32_t &m, uint32_t &l, int &sm,
+                                         int &sl) {
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    h = m = l = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int xi = max(-8388607, min(8388607, (int)rintf(e[j] * inv)));
+        const uint32_t u = (uint32_t)xi;
+        h |= ((u >> 16) & 0xFFu) << (8 * j);
+        m |= ((u >> 8) & 0xFFu) << (8 * j);
+        l |= (u & 0xFFu) << (8 * j);
+        sm += (int)((u >> 8) & 0xFFu);
+        sl += (int)(u & 0xFFu);
+    }
+}
+
+// Rows of one column tile (gw == 1) need all of x in every wave of the
+// workgroup: there the waves convert x once, cooperatively, into an LDS image
+// with one scale per 256 columns, and each lane loads its registers from it.
 // LDS image: hi | mid | lo  [cols_pad] int8 each, scale[nblk] f32 (= a),
 // xs16[cols_pad/16] f32 (exact fp32 sums of 16 x), smid32 / slo32
 // [cols_pad/32] i32 (sums of the mid / lo limbs over 32 columns, for the
@@ -120,13 +160,6 @@ struct XImage {
     __device__ int *slo32() const { return smid32() + 8 * nblk; }
     static __host__ __device__ size_t bytes(int nblk) { return (size_t)nblk * (768 + 4 + 64 + 32 + 32); }
 };
-
-// cols is a multiple of 32: a float4 is either wholly inside or wholly past
-// the end.  The load is clamped in range; x_quant_block zeroes the float4s
-// that lie past the end (at use, so the load is not waited for here).
-__device__ __forceinline__ float4 x_load4(const float *X, int cols, int c) {
-    return *reinterpret_cast<const float4 *>(X + min(c, cols - 4));
-}
 
 __device__ __forceinline__ void x_quant_block(const XImage &im, int b, float4 v) {
     const int lane = threadIdx.x & 63;
@@ -202,8 +235,10 @@ template <int N> struct XLimbs {
 
 template <int T> struct XRegs;
 
-template <> struct XRegs<12> : XLimbs<16> {  // 64 columns: sub-blocks 2g ([0..7]) and 2g+1 ([8..15])
+// Q4_K: 64 columns b*256 + 64g .. +64, i.e. sub-blocks 2g ([0..7]) and 2g+1 ([8..15])
+template <> struct XRegs<12> : XLimbs<16> {
     float a, xs0, xs1;
+    static __device__ __forceinline__ int col(int b, int g, int k) { return b * 256 + 64 * g + 4 * k; }
     __device__ void load(const XImage &im, int b, int g, bool act) {
         load_run(im, (b * 256 + 64 * g) / 4, 0, 16);
         const float4 s = *reinterpret_cast<const float4 *>(im.xs16() + b * 16 + 4 * g);
@@ -211,10 +246,30 @@ template <> struct XRegs<12> : XLimbs<16> {  // 64 columns: sub-blocks 2g ([0..7
         xs0 = act ? s.x + s.y : 0.f;
         xs1 = act ? s.z + s.w : 0.f;
     }
+    __device__ void convert(const float4 (&v)[16], bool act) {
+        float mx = 0.f, s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            mx = fmaxf(mx, amax4(v[k]));
+            const float s = (v[k].x + v[k].y) + (v[k].z + v[k].w);
+            if (k < 8) s0 += s; else s1 += s;
+        }
+        const float inv = mx > 0.f ? kMaxInt / mx : 0.f;
+        int sm = 0, sl = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) to_limbs(v[k], inv, h[k], m[k], l[k], sm, sl);
+        a = act ? mx * (1.f / kMaxInt) : 0.f;
+        xs0 = act ? s0 : 0.f;
+        xs1 = act ? s1 : 0.f;
+    }
 };
 
-template <> struct XRegs<14> : XLimbs<16> {  // runs k = 0..3 of 16 columns: b*256 + hh*128 + 32k + l0
+// Q6_K: runs k = 0..3 of 16 columns b*256 + hh*128 + 32k + l0 (hh = g/2, l0 = 16(g&1))
+template <> struct XRegs<14> : XLimbs<16> {
     float a, m32[4];
+    static __device__ __forceinline__ int col(int b, int g, int k) {
+        return b * 256 + (g >> 1) * 128 + 32 * (k >> 2) + 16 * (g & 1) + 4 * (k & 3);
+    }
     __device__ void load(const XImage &im, int b, int g, bool act) {
         const int hh = g >> 1, l0 = 16 * (g & 1);
 #pragma unroll
@@ -225,16 +280,43 @@ template <> struct XRegs<14> : XLimbs<16> {  // runs k = 0..3 of 16 columns: b*2
         }
         a = act ? im.scale()[b] : 0.f;
     }
+    __device__ void convert(const float4 (&v)[16], bool act) {
+        float mx = 0.f, s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            mx = fmaxf(mx, amax4(v[k]));
+            s[k >> 2] += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+        }
+        const float inv = mx > 0.f ? kMaxInt / mx : 0.f;
+        int sm = 0, sl = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) to_limbs(v[k], inv, h[k], m[k], l[k], sm, sl);
+        a = act ? mx * (1.f / kMaxInt) : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) m32[r] = act ? -32.f * s[r] : 0.f;
+    }
 };
 
-template <> struct XRegs<8> : XLimbs<8> {  // 32 columns of block b
+// Q8_0: the 32 columns of block b
+template <> struct XRegs<8> : XLimbs<8> {
     float a;
     int sm, sl;  // limb sums, for the +128 bias of the signed quants
+    static __device__ __forceinline__ int col(int b, int, int k) { return b * 32 + 4 * k; }
     __device__ void load(const XImage &im, int b, int, bool act) {
         load_run(im, b * 8, 0, 8);
         a = act ? im.scale()[b / 8] : 0.f;
         sm = im.smid32()[b];
         sl = im.slo32()[b];
+    }
+    __device__ void convert(const float4 (&v)[8], bool act) {
+        float mx = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) mx = fmaxf(mx, amax4(v[k]));
+        const float inv = mx > 0.f ? kMaxInt / mx : 0.f;
+        sm = sl = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) to_limbs(v[k], inv, h[k], m[k], l[k], sm, sl);
+        a = act ? mx * (1.f / kMaxInt) : 0.f;
     }
 };
 
@@ -362,7 +444,7 @@ __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
     return p;
 }
 
-template <int T, int R>
+template <int T, int R, bool SX>  // SX: one column tile, x shared through an LDS image
 __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
     using F = Fmt<T>;
     constexpr int K = (F::CH + 63) / 64;  // 16-byte loads per lane per row
@@ -372,9 +454,10 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
     const int lane = threadIdx.x & 63;
     const int nb = args.nb, nrows = args.nrows, gw = args.gw, tb = args.tb;
     const size_t pitch = args.pitch;
+    constexpr bool shared_x = SX;  // gw == 1: every wave needs all of x
     const int nblk = (args.cols + 255) / 256;
     XImage im{args.cols, nblk, lds};
-    uint4 *stage = reinterpret_cast<uint4 *>(lds + ((XImage::bytes(nblk) + 15) & ~size_t(15)));
+    uint4 *stage = reinterpret_cast<uint4 *>(lds + (shared_x ? (XImage::bytes(nblk) + 15) & ~size_t(15) : 0));
     uint4 *buf0 = stage + wave * R * F::CH;
     float *part = reinterpret_cast<float *>(stage + 4 * R * F::CH);  // [2][4][R]
 
@@ -397,11 +480,18 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
     for (int k = 0; k < K; k++) ld_off[k] = 16 * min(lane + 64 * k, nch - 1);
     const int lane_blk = (act ? blk : 0) * F::BB;
 
-    // 1. first x loads (before any weight load, so waiting for x does not
-    //    wait for the weight stream); up to 4 blocks of 256 per wave
-    float4 xv[4];
+    // 1. x loads, before any weight load so that waiting for x does not wait
+    //    for the weight stream: with one column tile, up to 4 blocks of 256
+    //    per wave for the shared image; otherwise this lane's own columns
+    constexpr int NX = SX ? 4 : (T == 8 ? 8 : 16);
+    float4 xv[NX];
+    if constexpr (shared_x) {
 #pragma unroll
-    for (int k = 0; k < 4; k++) xv[k] = x_load4(args.x, args.cols, (wave + 4 * k) * 256 + lane * 4);
+        for (int k = 0; k < 4; k++) xv[k] = x_load4(args.x, args.cols, (wave + 4 * k) * 256 + lane * 4);
+    } else {
+#pragma unroll
+        for (int k = 0; k < NX; k++) xv[k] = x_load4(args.x, args.cols, XRegs<T>::col(b, sub, k));
+    }
     asm volatile("" ::: "memory");
 
     // 2. weight loads.  Byte offsets are relative to args.w, which is 256-byte
@@ -431,14 +521,21 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
     issue(grp);
     asm volatile("" ::: "memory");
 
-    // 3. quantize x into LDS (blocks beyond the first 4 per wave load now)
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-        if (wave + 4 * k < nblk) x_quant_block(im, wave + 4 * k, xv[k]);
-    for (int bx = wave + 16; bx < nblk; bx += 4) x_quant_block(im, bx, x_load4(args.x, args.cols, bx * 256 + lane * 4));
-    __syncthreads();
+    // 3. x into registers
     XRegs<T> xr;
-    xr.load(im, b, sub, act);
+    if constexpr (shared_x) {
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (wave + 4 * k < nblk) x_quant_block(im, wave + 4 * k, xv[k]);
+        for (int bx = wave + 16; bx < nblk; bx += 4)
+            x_quant_block(im, bx, x_load4(args.x, args.cols, bx * 256 + lane * 4));
+        __syncthreads();
+        xr.load(im, b, sub, act);
+    } else {
+#pragma unroll
+        for (int k = 0; k < NX; k++) xv[k] = x_mask4(xv[k], args.cols, XRegs<T>::col(b, sub, k));
+        xr.convert(xv, act);
+    }
 
     // 4. pipelined walk over row groups
     park(buf0);
@@ -494,6 +591,18 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
     }
 }
 
+template <int T, int R, bool SX>
+hipError_t launch_staged_sx(const StagedArgs &sa, size_t lds, int wgs, hipStream_t s) {
+    static bool attr_set = [] {
+        // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950)
+        return hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_staged<T, R, SX>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    }();
+    (void)attr_set;
+    gemv_staged<T, R, SX><<<wgs, 256, lds, s>>>(sa);
+    return hipGetLastError();
+}
+
 template <int T, int R>
 hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
     using F = Fmt<T>;
@@ -501,7 +610,8 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
     sa.gw = nb <= F::TBMAX ? 1 : nb <= 2 * F::TBMAX ? 2 : 4;
     sa.tb = (nb + sa.gw - 1) / sa.gw;
     const int nblk = (sa.cols + 255) / 256;
-    const size_t lds = ((XImage::bytes(nblk) + 15) & ~size_t(15)) + (size_t)4 * R * F::CH * 16 + 2 * 4 * R * 4;
+    const size_t lds = (sa.gw == 1 ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)4 * R * F::CH * 16 +
+                       2 * 4 * R * 4;
     const int slots = 4 / sa.gw;
     const int ngroups = (sa.nrows + R - 1) / R;
     // persistent grid: as many workgroups as fit at once, capped by the work
@@ -510,14 +620,7 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
     int wgs = 256 * per_cu;
     const int need = (ngroups + slots - 1) / slots;
     if (wgs > need) wgs = need;
-    static bool attr_set = [] {
-        // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950)
-        return hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_staged<T, R>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
-    }();
-    (void)attr_set;
-    gemv_staged<T, R><<<wgs, 256, lds, s>>>(sa);
-    return hipGetLastError();
+    return sa.gw == 1 ? launch_staged_sx<T, R, true>(sa, lds, wgs, s) : launch_staged_sx<T, R, false>(sa, lds, wgs, s);
 }
 
 }  // namespace
