@@ -161,12 +161,25 @@ struct XImage {
     static __host__ __device__ size_t bytes(int nblk) { return (size_t)nblk * (768 + 4 + 64 + 32 + 32); }
 };
 
+// sum of v over the 4 lanes of a quad, in every lane of the quad
+__device__ __forceinline__ float quad_sum(float v) {
+    int x = __builtin_bit_cast(int, v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true));  // quad_perm 1,0,3,2
+    x = __builtin_bit_cast(int, v);
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true));  // 2,3,0,1
+}
+// sum of v over the 8 lanes 8k .. 8k+7, in every one of them
+__device__ __forceinline__ int oct_sum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);   // quad_perm 1,0,3,2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);   // quad_perm 2,3,0,1
+    return v + __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true);  // row_half_mirror
+}
+
 __device__ __forceinline__ void x_quant_block(const XImage &im, int b, float4 v) {
     const int lane = threadIdx.x & 63;
     if (b * 256 + lane * 4 >= im.cols) v = make_float4(0.f, 0.f, 0.f, 0.f);
     float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     m = wave_max_all(m);
-    constexpr float kMaxInt = 8388607.f;  // 2^23 - 1
     const float a = m * (1.f / kMaxInt);
     const float inv = m > 0.f ? kMaxInt / m : 0.f;
     const float e[4] = {v.x, v.y, v.z, v.w};
@@ -185,16 +198,12 @@ __device__ __forceinline__ void x_quant_block(const XImage &im, int b, float4 v)
     im.hi()[b * 64 + lane] = ph;
     im.mid()[b * 64 + lane] = pm;
     im.lo()[b * 64 + lane] = pl;
-    float s = (v.x + v.y) + (v.z + v.w);
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    // sums over 4 lanes (16 columns) and 8 lanes (32 columns) with DPP
+    // (quad_perm and row_half_mirror) rather than LDS permutes
+    const float s = quad_sum((v.x + v.y) + (v.z + v.w));
     if ((lane & 3) == 0) im.xs16()[b * 16 + (lane >> 2)] = s;
-    sm += __shfl_xor(sm, 1);
-    sl += __shfl_xor(sl, 1);
-    sm += __shfl_xor(sm, 2);
-    sl += __shfl_xor(sl, 2);
-    sm += __shfl_xor(sm, 4);
-    sl += __shfl_xor(sl, 4);
+    sm = oct_sum(sm);
+    sl = oct_sum(sl);
     if ((lane & 7) == 0) {
         im.smid32()[b * 8 + (lane >> 3)] = sm;
         im.slo32()[b * 8 + (lane >> 3)] = sl;
