@@ -147,6 +147,43 @@ int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *
  * caller-provided device buffer of rawByteCount(type, n) bytes. */
 int jh_quantize_dev(int ggml_type, const float *d_src, int64_t n, void *d_dst, void *stream);
 
+/* ---- The rest of a Llama decode step, device-resident.  All pointers are
+ * device pointers; the device is the caller's current device; work is
+ * enqueued on `stream` (NULL: the null stream).  The decode position is a
+ * device int (d_pos) so that a captured graph of a step can be replayed with
+ * the position advanced on the device (jh_pos_increment_dev).  These have no
+ * C counterpart in the reference: each restates one Java method of
+ * LlamaTransformerHandler, cited per function, for a device-activation path
+ * beside the MatVec interface. */
+
+/* out = rmsNorm(v, w, eps) with v = x + res (res may be NULL: v = x); when
+ * x_out is not NULL it receives v (x_out may equal x: in-place residual).
+ * rmsNorm: LlamaTransformerHandler.java:818-826; the residual adds of
+ * transformerLayer :778, :783.  n <= 1 << 20. */
+int jh_rmsnorm_dev(const float *x, const float *res, const float *w, int n, float eps, float *x_out, float *out,
+                   void *stream);
+
+/* Rotary embedding at position *d_pos (adjacent pairs) of q in place and of
+ * k into k_cache[pos], and v copied into v_cache[pos]; caches hold max_seq
+ * rows of n_kv_heads * head_dim floats.  rope: LlamaTransformerHandler.java:
+ * 1657-1671; the cache stores of transformerLayer :769-770. */
+int jh_rope_kv_dev(float *q, const float *k, const float *v, int n_heads, int n_kv_heads, int head_dim,
+                   const int *d_pos, int max_seq, float theta, float *k_cache, float *v_cache, void *stream);
+
+/* Grouped-query attention of q over cache positions 0 .. *d_pos, output
+ * [n_heads * head_dim].  gqa + softmax: LlamaTransformerHandler.java:1678-1731.
+ * Uses a per-stream library workspace (allocated on first use, JH_ENOMEM
+ * with "hipMalloc" in the message on failure). */
+int jh_attention_dev(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,
+                     int head_dim, const int *d_pos, int max_seq, float *out, void *stream);
+
+/* out = silu(gate) * up.  silu and ffn: LlamaTransformerHandler.java:1733-1735,
+ * 796-797. */
+int jh_silu_mul_dev(const float *gate, const float *up, int n, float *out, void *stream);
+
+/* *d_pos += delta, on the device (for replaying a captured decode step). */
+int jh_pos_increment_dev(int *d_pos, int delta, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -570,4 +570,72 @@ int jh_quantize_dev(int type, const float *d_src, int64_t n, void *d_dst, void *
     return ok();
 }
 
+// ---- the rest of the decode step
+
+int jh_rmsnorm_dev(const float *x, const float *res, const float *w, int n, float eps, float *x_out, float *out,
+                   void *stream) {
+    if (n < 1 || n > (1 << 20)) return fail(JH_EINVAL, "n=%d outside [1, 2^20]", n);
+    if (!x || !w || !out) return fail(JH_EINVAL, "x, w and out must not be null");
+    if (out == x || (x_out && out == x_out)) return fail(JH_EINVAL, "out must not alias x or x_out");
+    hipError_t e = jh::launch_rmsnorm(x, res, w, n, eps, x_out, out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("rmsnorm launch", e);
+    return ok();
+}
+
+static int check_heads(int n_heads, int n_kv_heads, int head_dim, int max_seq) {
+    if (n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads)
+        return fail(JH_EINVAL, "n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
+    if (head_dim < 2 || head_dim % 2 || head_dim > 256)
+        return fail(JH_EINVAL, "head_dim=%d must be even and in [2, 256]", head_dim);
+    if (max_seq < 1) return fail(JH_EINVAL, "max_seq=%d must be >= 1", max_seq);
+    return JH_OK;
+}
+
+int jh_rope_kv_dev(float *q, const float *k, const float *v, int n_heads, int n_kv_heads, int head_dim,
+                   const int *d_pos, int max_seq, float theta, float *k_cache, float *v_cache, void *stream) {
+    int rc;
+    if ((rc = check_heads(n_heads, n_kv_heads, head_dim, max_seq))) return rc;
+    if (!q || !k || !v || !d_pos || !k_cache || !v_cache) return fail(JH_EINVAL, "pointers must not be null");
+    hipError_t e = jh::launch_rope_kv(q, k, v, n_heads, n_kv_heads, head_dim, d_pos, max_seq, theta, k_cache, v_cache,
+                                      (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("rope_kv launch", e);
+    return ok();
+}
+
+int jh_attention_dev(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,
+                     int head_dim, const int *d_pos, int max_seq, float *out, void *stream) {
+    int rc;
+    if ((rc = check_heads(n_heads, n_kv_heads, head_dim, max_seq))) return rc;
+    if (!q || !k_cache || !v_cache || !d_pos || !out) return fail(JH_EINVAL, "pointers must not be null");
+    if (jh::attention_lds_bytes(n_heads, n_kv_heads, head_dim) > 160 * 1024)
+        return fail(JH_EUNSUPPORTED, "n_heads / n_kv_heads = %d too large for one workgroup's LDS",
+                    n_heads / n_kv_heads);
+    int dev = 0;
+    JH_HIP("hipGetDevice", hipGetDevice(&dev));
+    void *ws = nullptr;
+    if ((rc = stream_workspace(dev, (hipStream_t)stream, jh::attention_workspace_bytes(n_heads, head_dim, max_seq),
+                               &ws)))
+        return rc;
+    hipError_t e = jh::launch_attention(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos, max_seq, out, ws,
+                                        (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("attention launch", e);
+    return ok();
+}
+
+int jh_silu_mul_dev(const float *gate, const float *up, int n, float *out, void *stream) {
+    if (n < 0) return fail(JH_EINVAL, "n=%d must be >= 0", n);
+    if (n == 0) return ok();
+    if (!gate || !up || !out) return fail(JH_EINVAL, "pointers must not be null");
+    hipError_t e = jh::launch_silu_mul(gate, up, n, out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("silu_mul launch", e);
+    return ok();
+}
+
+int jh_pos_increment_dev(int *d_pos, int delta, void *stream) {
+    if (!d_pos) return fail(JH_EINVAL, "d_pos must not be null");
+    hipError_t e = jh::launch_pos_increment(d_pos, delta, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("pos_increment launch", e);
+    return ok();
+}
+
 }  // extern "C"

@@ -69,4 +69,16 @@ hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float 
 // n fp32 values -> packed blocks with the LoraMerge quantizers.
 hipError_t launch_quantize(int type, const float *src, int64_t n, uint8_t *dst, hipStream_t s);
 
+// ---- the rest of a Llama decode step (jh_decode.hip); d_pos is a device int
+hipError_t launch_rmsnorm(const float *x, const float *res, const float *w, int n, float eps, float *x_out,
+                          float *out, hipStream_t s);
+hipError_t launch_rope_kv(float *q, const float *k, const float *v, int n_heads, int n_kv_heads, int head_dim,
+                          const int *d_pos, int max_seq, float theta, float *k_cache, float *v_cache, hipStream_t s);
+size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq);
+size_t attention_lds_bytes(int n_heads, int n_kv_heads, int head_dim);
+hipError_t launch_attention(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,
+                            int head_dim, const int *d_pos, int max_seq, float *out, void *workspace, hipStream_t s);
+hipError_t launch_silu_mul(const float *gate, const float *up, int n, float *out, hipStream_t s);
+hipError_t launch_pos_increment(int *d_pos, int delta, hipStream_t s);
+
 }  // namespace jh

@@ -1,0 +1,242 @@
+"""Device-resident Llama decode step over libjunohip.
+
+Mirrors the reference's forward pass (paths under
+/root/reference/node/src/main/java/cab/ml/juno/node/):
+
+* ``LlamaConfig``      the LlamaConfig record (LlamaConfig.java:29-40; defaults
+                       rmsNormEps 1e-5, ropeTheta 10000, :105-115)
+* ``LlamaWeights``     the handler's per-layer tensors (attn / ffn norms and the
+                       seven projections, LlamaTransformerHandler.java:743-800), the
+                       output norm and output projection, device-resident and packed
+* ``LlamaDecoder``     ``forward`` = getInitialActivation + runLayers +
+                       outputProjection (LlamaTransformerHandler.java:603-810) for one
+                       token at ``pos``, with the KV cache in HBM; ``capture`` records a
+                       whole step as one HIP graph that advances the position on the
+                       device, so steps replay without host work.
+
+Each layer is the reference's transformerLayer: rmsNorm -> Q, K, V -> rope and
+KV append -> gqa -> O + residual -> rmsNorm -> gate, up -> silu(gate) * up ->
+down + residual.  The residual adds are fused into the following rmsNorm.
+Everything runs on HIP kernels of libjunohip; there is no host fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+from .matvec import (Q4_K, Q6_K, DeviceQuantMatrix, GpuContext, IllegalArgumentException, _check)
+
+_V = ctypes.c_void_p
+
+
+def _torch():
+    import torch  # device memory and streams: plumbing around the HIP library
+    return torch
+
+
+@dataclass
+class LlamaConfig:
+    hidden_dim: int
+    num_layers: int
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    intermediate_size: int
+    vocab_size: int
+    rms_norm_eps: float = 1e-5
+    rope_theta: float = 10000.0
+
+    @property
+    def kv_dim(self) -> int:
+        return self.num_kv_heads * self.head_dim
+
+    @property
+    def gqa_ratio(self) -> int:
+        return self.num_heads // self.num_kv_heads
+
+    def validate(self) -> None:
+        if self.num_heads % self.num_kv_heads:
+            raise IllegalArgumentException("numHeads must be a multiple of numKvHeads")
+        if self.num_heads * self.head_dim != self.hidden_dim:
+            raise IllegalArgumentException("numHeads * headDim must equal hiddenDim")
+
+
+# Q4_K_M assignment used by the benchmark configs: Q6_K for attn_v, ffn_down
+# and the output projection, Q4_K elsewhere.
+Q4_K_M = {"q": Q4_K, "k": Q4_K, "v": Q6_K, "o": Q4_K, "gate": Q4_K, "up": Q4_K, "down": Q6_K, "output": Q6_K}
+
+
+def matrix_shapes(cfg: LlamaConfig) -> dict:
+    H, I, KV = cfg.hidden_dim, cfg.intermediate_size, cfg.kv_dim
+    return {"q": (H, H), "k": (KV, H), "v": (KV, H), "o": (H, H), "gate": (I, H), "up": (I, H), "down": (H, I)}
+
+
+@dataclass
+class LlamaLayerWeights:
+    attn_norm: object  # torch float32 [hidden] on the device
+    ffn_norm: object
+    mats: dict          # name -> DeviceQuantMatrix
+
+
+@dataclass
+class LlamaWeights:
+    cfg: LlamaConfig
+    layers: list
+    output_norm: object
+    output: DeviceQuantMatrix
+    keep: list = field(default_factory=list)
+
+    def close(self) -> None:
+        for lw in self.layers:
+            for m in lw.mats.values():
+                m.close()
+        self.output.close()
+
+    @classmethod
+    def random(cls, cfg: LlamaConfig, types: dict = Q4_K_M, seed: int = 0, device: int = 0,
+               std: float = 0.02) -> "LlamaWeights":
+        """Random-init weights ~ N(0, std) drawn on the device and packed with the
+        device quantizer (bit-identical to LoraMerge's quantizers); norm weights 1 + N(0, 0.1^2)."""
+        torch = _torch()
+        cfg.validate()
+        be = GpuContext.shared(device).create_mat_vec()
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        dev = torch.device("cuda", device)
+        layers = []
+
+        def qmat(qtype, rows, cols):
+            w = torch.randn(rows * cols, generator=g, device=dev, dtype=torch.float32).mul_(std)
+            m = be.quantize_dev(qtype, w.data_ptr(), rows, cols)
+            torch.cuda.synchronize()
+            del w
+            return m
+
+        def norm():
+            return (1.0 + 0.1 * torch.randn(cfg.hidden_dim, generator=g, device=dev, dtype=torch.float32)).contiguous()
+
+        shapes = matrix_shapes(cfg)
+        for _ in range(cfg.num_layers):
+            mats = {n: qmat(types[n], *shapes[n]) for n in shapes}
+            layers.append(LlamaLayerWeights(norm(), norm(), mats))
+        out = qmat(types["output"], cfg.vocab_size, cfg.hidden_dim)
+        return cls(cfg, layers, norm(), out)
+
+    @classmethod
+    def from_packed(cls, cfg: LlamaConfig, layers: list, output_norm, output_raw, output_type: int,
+                    device: int = 0) -> "LlamaWeights":
+        """Upload packed GGUF tensors unchanged.  layers[i] holds 'attn_norm',
+        'ffn_norm' (float32 [hidden]) and, per projection m in q k v o gate up down,
+        'w' + m (packed bytes) and 'type_' + m."""
+        torch = _torch()
+        cfg.validate()
+        be = GpuContext.shared(device).create_mat_vec()
+        dev = torch.device("cuda", device)
+        vec = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+        shapes = matrix_shapes(cfg)
+        out_layers = []
+        for lw in layers:
+            mats = {m: be.upload_quant(lw["type_" + m], *shapes[m], lw["w" + m]) for m in shapes}
+            out_layers.append(LlamaLayerWeights(vec(lw["attn_norm"]), vec(lw["ffn_norm"]), mats))
+        out = be.upload_quant(output_type, cfg.vocab_size, cfg.hidden_dim, output_raw)
+        return cls(cfg, out_layers, vec(output_norm), out)
+
+
+class LlamaDecoder:
+    """One request's decode state: KV cache [layers][max_seq][kv_dim] in HBM,
+    activation buffers and the device position."""
+
+    def __init__(self, weights: LlamaWeights, max_seq: int, device: int = 0):
+        torch = _torch()
+        self.w, self.cfg, self.max_seq = weights, weights.cfg, max_seq
+        c = self.cfg
+        self.L = _lib.load()
+        dev = torch.device("cuda", device)
+        f32 = dict(device=dev, dtype=torch.float32)
+        self.k_cache = torch.zeros(c.num_layers, max_seq, c.kv_dim, **f32)
+        self.v_cache = torch.zeros(c.num_layers, max_seq, c.kv_dim, **f32)
+        self.x = torch.zeros(c.hidden_dim, **f32)      # residual stream
+        self.xn = torch.zeros(c.hidden_dim, **f32)     # normalised input of a projection
+        self.q = torch.zeros(c.hidden_dim, **f32)
+        self.k = torch.zeros(c.kv_dim, **f32)
+        self.v = torch.zeros(c.kv_dim, **f32)
+        self.att = torch.zeros(c.hidden_dim, **f32)
+        self.proj = torch.zeros(c.hidden_dim, **f32)
+        self.gate = torch.zeros(c.intermediate_size, **f32)
+        self.up = torch.zeros(c.intermediate_size, **f32)
+        self.hid = torch.zeros(c.intermediate_size, **f32)
+        self.logits = torch.zeros(c.vocab_size, **f32)
+        self.pos = torch.zeros(1, device=dev, dtype=torch.int32)
+
+    # ---------------------------------------------------------------- enqueue
+    def _group(self, mats, xs, ys, s) -> None:
+        n = len(mats)
+        handles = (_V * n)(*[m.handle for m in mats])
+        dx = (_V * n)(*[x.data_ptr() for x in xs])
+        dy = (_V * n)(*[y.data_ptr() for y in ys])
+        _check(self.L.jh_qmatvec_group_dev(n, handles, dx, dy, s))
+
+    def enqueue_step(self, stream=None, advance: bool = False) -> None:
+        """Enqueue one decode step on ``stream`` (a torch stream or None for the
+        current one): x (the input activation) -> logits at position *pos.  With
+        advance, *pos += 1 on the device at the end (for graph replay)."""
+        torch = _torch()
+        c, L = self.cfg, self.L
+        s = _V((stream or torch.cuda.current_stream()).cuda_stream)
+        P = lambda t: _V(t.data_ptr())
+        eps, nh, nkv, hd, H = c.rms_norm_eps, c.num_heads, c.num_kv_heads, c.head_dim, c.hidden_dim
+        for li, lw in enumerate(self.w.layers):
+            if li == 0:  # rmsNorm(x) (LlamaTransformerHandler.java:748)
+                _check(L.jh_rmsnorm_dev(P(self.x), None, P(lw.attn_norm), H, eps, None, P(self.xn), s))
+            else:        # previous layer's x2 + ffnOut (:784), then this layer's rmsNorm
+                _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(lw.attn_norm), H, eps, P(self.x), P(self.xn), s))
+            m = lw.mats
+            self._group([m["q"], m["k"], m["v"]], [self.xn] * 3, [self.q, self.k, self.v], s)
+            _check(L.jh_rope_kv_dev(P(self.q), P(self.k), P(self.v), nh, nkv, hd, P(self.pos), self.max_seq,
+                                    c.rope_theta, P(self.k_cache[li]), P(self.v_cache[li]), s))
+            _check(L.jh_attention_dev(P(self.q), P(self.k_cache[li]), P(self.v_cache[li]), nh, nkv, hd, P(self.pos),
+                                      self.max_seq, P(self.att), s))
+            self._group([m["o"]], [self.att], [self.proj], s)
+            # x2 = x + attnProj (:778); rmsNorm(x2) (:781)
+            _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(lw.ffn_norm), H, eps, P(self.x), P(self.xn), s))
+            self._group([m["gate"], m["up"]], [self.xn] * 2, [self.gate, self.up], s)
+            _check(L.jh_silu_mul_dev(P(self.gate), P(self.up), c.intermediate_size, P(self.hid), s))
+            self._group([m["down"]], [self.hid], [self.proj], s)
+        # final residual, rmsNorm(x, outputNorm) and the output projection (:803-810)
+        _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(self.w.output_norm), H, eps, P(self.x), P(self.xn), s))
+        self._group([self.w.output], [self.xn], [self.logits], s)
+        if advance:
+            _check(L.jh_pos_increment_dev(P(self.pos), 1, s))
+
+    # ---------------------------------------------------------------- host API
+    def forward(self, activation, pos: int) -> np.ndarray:
+        """logits for one token whose input activation (the embedding row, or the
+        previous node's activations) is ``activation`` at position ``pos``."""
+        torch = _torch()
+        a = np.ascontiguousarray(activation, dtype=np.float32).reshape(-1)
+        if a.size != self.cfg.hidden_dim:
+            raise IllegalArgumentException(f"activation length {a.size} != hiddenDim {self.cfg.hidden_dim}")
+        if not 0 <= pos < self.max_seq:
+            raise IllegalArgumentException(f"pos {pos} outside [0, {self.max_seq})")
+        self.x.copy_(torch.from_numpy(a))
+        self.pos.fill_(pos)
+        self.enqueue_step()
+        torch.cuda.synchronize()
+        return self.logits.cpu().numpy()
+
+    def capture(self, stream):
+        """A HIP graph of one step that also advances *pos; replay it after
+        writing the next activation into ``self.x``.  Capturing runs one eager
+        warm-up step first (it allocates the library's stream workspace outside
+        the capture), which overwrites x, the logits and the KV row at *pos."""
+        torch = _torch()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            self.enqueue_step(stream)  # warm-up: workspaces are allocated outside the capture
+            stream.synchronize()
+            with torch.cuda.graph(g, stream=stream):
+                self.enqueue_step(stream, advance=True)
+        return g

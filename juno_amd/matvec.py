@@ -168,6 +168,19 @@ class DeviceQuantMatrix:
         _check(_lib.load().jh_qmat_info(self.handle, None, None, None, ctypes.byref(n), None))
         return n.value
 
+    def packed_bytes(self) -> np.ndarray:
+        """The packed GGUF bytes, copied back to the host (the inverse of upload_quant)."""
+        import torch  # the HIP runtime torch loaded; device memory plumbing
+        n = self.nbytes()
+        tmp = torch.empty(n, dtype=torch.uint8, device="cuda")
+        hip = ctypes.CDLL("libamdhip64.so.7")  # already loaded by torch (and by libjunohip)
+        torch.cuda.synchronize()
+        rc = hip.hipMemcpy(ctypes.c_void_p(tmp.data_ptr()), ctypes.c_void_p(self.device_pointer()),
+                           ctypes.c_size_t(n), 3)  # hipMemcpyDeviceToDevice
+        if rc != 0:
+            raise IllegalStateException(f"hipMemcpy failed: rc={rc}")
+        return tmp.cpu().numpy()
+
     def close(self) -> None:
         with self._mu:
             if self._h is not None:

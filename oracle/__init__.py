@@ -33,6 +33,19 @@ BLOCK_BYTES = {F32: 4, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 _lib = None
 
 
+class LlamaDimsC(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("n_heads", ctypes.c_int), ("n_kv_heads", ctypes.c_int),
+                ("head_dim", ctypes.c_int), ("ffn", ctypes.c_int), ("eps", ctypes.c_float),
+                ("theta", ctypes.c_float)]
+
+
+class LlamaLayerC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("attn_norm", "ffn_norm", "wq", "wk", "wv", "wo", "wgate", "wup",
+                                                "wdown")] + \
+               [(n, ctypes.c_int) for n in ("type_q", "type_k", "type_v", "type_o", "type_gate", "type_up",
+                                             "type_down")]
+
+
 def build() -> str:
     """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
     subprocess.run(["make", "-s", "-C", HERE], check=True)
@@ -62,6 +75,16 @@ def lib() -> ctypes.CDLL:
         L.or_matvec.argtypes = [ctypes.c_int, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                 P, ctypes.c_int]
         L.or_quantize.argtypes = [ctypes.c_int, P, ctypes.c_int64, P]
+        I, F = ctypes.c_int, ctypes.c_float
+        L.or_rmsnorm.argtypes = [P, P, I, F, P]
+        L.or_rope.argtypes = [P, I, I, I, F]
+        L.or_softmax.argtypes = [P, I]
+        L.or_gqa.argtypes = [P, P, P, I, I, I, I, P]
+        L.or_silu.argtypes = [F]
+        L.or_silu.restype = F
+        L.or_silu_mul.argtypes = [P, P, I, P]
+        L.or_add.argtypes = [P, P, I, P]
+        L.or_llama_layer.argtypes = [ctypes.POINTER(LlamaLayerC), ctypes.POINTER(LlamaDimsC), P, I, P, P, I]
         _lib = L
     return _lib
 
@@ -136,3 +159,76 @@ def quantize(qtype: int, data: np.ndarray) -> np.ndarray:
     if lib().or_quantize(qtype, _ptr(data), n, _ptr(out)) != 0:
         raise ValueError(f"quantize: unsupported type {qtype}")
     return out
+
+
+# ---------------------------------------------------------------- decode step (juno_oracle_decode.c)
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    x, w = _f32(x), _f32(w)
+    out = np.empty_like(x)
+    lib().or_rmsnorm(_ptr(x), _ptr(w), x.size, eps, _ptr(out))
+    return out
+
+
+def rope(x, pos: int, n_heads: int, head_dim: int, theta: float) -> np.ndarray:
+    """Returns a rotated copy (the reference rotates in place)."""
+    y = _f32(x).copy()
+    lib().or_rope(_ptr(y), pos, n_heads, head_dim, theta)
+    return y
+
+
+def softmax(s) -> np.ndarray:
+    y = _f32(s).copy()
+    lib().or_softmax(_ptr(y), y.size)
+    return y
+
+
+def gqa(q, k_cache, v_cache, n_heads: int, n_kv_heads: int, head_dim: int, seq_len: int) -> np.ndarray:
+    q, k_cache, v_cache = _f32(q), _f32(k_cache), _f32(v_cache)
+    out = np.empty(n_heads * head_dim, dtype=np.float32)
+    lib().or_gqa(_ptr(q), _ptr(k_cache), _ptr(v_cache), n_heads, n_kv_heads, head_dim, seq_len, _ptr(out))
+    return out
+
+
+def silu(x: float) -> float:
+    return lib().or_silu(x)
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    gate, up = _f32(gate), _f32(up)
+    out = np.empty_like(gate)
+    lib().or_silu_mul(_ptr(gate), _ptr(up), gate.size, _ptr(out))
+    return out
+
+
+def add(a, b) -> np.ndarray:
+    a, b = _f32(a), _f32(b)
+    out = np.empty_like(a)
+    lib().or_add(_ptr(a), _ptr(b), a.size, _ptr(out))
+    return out
+
+
+def llama_layer(layer: dict, dims: dict, x, pos: int, k_cache: np.ndarray, v_cache: np.ndarray,
+                nthreads: int = 0) -> np.ndarray:
+    """One transformerLayer; k_cache / v_cache (float32, [>= pos+1, kv_dim]) receive
+    this position's k and v in place.  layer holds 'attn_norm', 'ffn_norm' (float32)
+    and per matrix m in q,k,v,o,gate,up,down: 'w'+m packed bytes and 'type_'+m."""
+    keep = {}
+    def buf(a, dt):
+        arr = np.ascontiguousarray(a, dtype=dt)
+        keep[id(arr)] = arr
+        return _ptr(arr)
+    L = LlamaLayerC(attn_norm=buf(layer["attn_norm"], np.float32), ffn_norm=buf(layer["ffn_norm"], np.float32),
+                    **{"w" + m: buf(layer["w" + m], np.uint8) for m in ("q", "k", "v", "o", "gate", "up", "down")},
+                    **{"type_" + m: layer["type_" + m] for m in ("q", "k", "v", "o", "gate", "up", "down")})
+    D = LlamaDimsC(**dims)
+    y = _f32(x).copy()
+    assert k_cache.dtype == np.float32 and k_cache.flags.c_contiguous and v_cache.flags.c_contiguous
+    if lib().or_llama_layer(ctypes.byref(L), ctypes.byref(D), _ptr(y), pos, _ptr(k_cache), _ptr(v_cache),
+                            nthreads) != 0:
+        raise ValueError("llama_layer: unsupported matrix type")
+    return y

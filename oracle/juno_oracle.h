@@ -55,6 +55,32 @@ int or_matvec(int type, const uint8_t *raw, const float *x, int row_start, int r
  * multiple.  out must hold or_raw_byte_count(type, n) bytes. */
 int or_quantize(int type, const float *data, int64_t n, uint8_t *out);
 
+/* ---- the rest of the decode step (juno_oracle_decode.c) ---- */
+void  or_rmsnorm(const float *x, const float *w, int n, float eps, float *out);
+void  or_rope(float *x, int pos, int n_heads, int head_dim, float theta);
+void  or_softmax(float *s, int n);
+void  or_gqa(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,
+             int head_dim, int seq_len, float *out);
+float or_silu(float x);
+void  or_silu_mul(const float *gate, const float *up, int n, float *out);
+void  or_add(const float *a, const float *b, int n, float *out);
+
+typedef struct {
+    int hidden, n_heads, n_kv_heads, head_dim, ffn;
+    float eps, theta;
+} OrLlamaDims;
+
+typedef struct {
+    const float *attn_norm, *ffn_norm;                               /* [hidden] */
+    const uint8_t *wq, *wk, *wv, *wo, *wgate, *wup, *wdown;           /* packed rows x cols */
+    int type_q, type_k, type_v, type_o, type_gate, type_up, type_down;
+} OrLlamaLayer;
+
+/* One transformer layer at position pos (x updated in place; k / v of this
+ * position written into the caches, which hold kv_dim floats per position). */
+int or_llama_layer(const OrLlamaLayer *L, const OrLlamaDims *D, float *x, int pos, float *k_cache,
+                   float *v_cache, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif
