@@ -310,6 +310,53 @@ def measured_traffic():
         return None, None
 
 
+def tinyllama_step(torch, stream, steps):
+    """TinyLlama-1.1B-shaped Q4_K_M full decode step (22 layers,
+    hidden 2048, 32 / 4 heads, head_dim 64, FFN 5632, vocab 32000; Q6_K for
+    attn_v, ffn_down and the output), B = 1, at position 511 over a KV cache
+    pre-filled with N(0, 1): every op of the step is a HIP kernel, the step is
+    one captured graph.  Also times the step's GEMV launches alone (the tok/s
+    bound the GEMVs set)."""
+    from juno_amd import decode as D
+    cfg = D.LlamaConfig(hidden_dim=2048, num_layers=22, num_heads=32, num_kv_heads=4, head_dim=64,
+                        intermediate_size=5632, vocab_size=32000)
+    w = D.LlamaWeights.random(cfg, seed=7)
+    dec = D.LlamaDecoder(w, max_seq=512)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(8)
+    dec.k_cache.normal_(generator=g)
+    dec.v_cache.normal_(generator=g)
+    dec.x.normal_(generator=g)
+    dec.pos.fill_(511)
+    x0 = dec.x.clone()
+    gemv_bytes = sum(m.nbytes() for lw in w.layers for m in lw.mats.values()) + w.output.nbytes()
+
+    def full():
+        dec.x.copy_(x0)  # the step updates the residual stream in place
+        dec.enqueue_step(stream)
+
+    def gemvs_only():
+        for lw in w.layers:
+            m = lw.mats
+            dec._group([m["q"], m["k"], m["v"]], [dec.xn] * 3, [dec.q, dec.k, dec.v], ctypes.c_void_p(stream.cuda_stream))
+            dec._group([m["o"]], [dec.att], [dec.proj], ctypes.c_void_p(stream.cuda_stream))
+            dec._group([m["gate"], m["up"]], [dec.xn] * 2, [dec.gate, dec.up], ctypes.c_void_p(stream.cuda_stream))
+            dec._group([m["down"]], [dec.hid], [dec.proj], ctypes.c_void_p(stream.cuda_stream))
+        dec._group([w.output], [dec.xn], [dec.logits], ctypes.c_void_p(stream.cuda_stream))
+
+    ms, _ = time_graph(torch, full, stream, steps, 3)
+    gemv_ms, _ = time_graph(torch, gemvs_only, stream, steps, 3)
+    out = {"config": "tinyllama-1.1b-q4_k_m-full-decode-step-b1-ctx512", "layers": cfg.num_layers,
+           "ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
+           "gemv_ms_per_step": round(gemv_ms, 4), "gemv_tok_s_bound": round(1e3 / gemv_ms, 1),
+           "gemv_bytes_per_step": gemv_bytes, "gemv_GB_s": round(gemv_bytes / (gemv_ms * 1e-3) / 1e9, 1),
+           "launches_per_step": cfg.num_layers * 9 + 2,
+           "ops": "rmsnorm(+residual), grouped q/k/v, rope + KV append + GQA (2 kernels), o, grouped gate/up, "
+                  "silu*up, down, final rmsnorm, output projection"}
+    w.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -365,6 +412,9 @@ def main():
                    "GB_s": round(sb32 / (ms32 * 1e-3) / 1e9, 1)}
         log(f"B=32 step: {ms32:.4f} ms  {batched}")
 
+    tiny = tinyllama_step(torch, stream, max(args.steps // 2, 10))
+    log(f"TinyLlama decode step: {tiny}")
+
     traffic, traffic_src = measured_traffic()
     parity = parity_spot_check(torch, L, mats, stream)
     log(f"parity spot check (layer-0 gate vs oracle): max rel-err {parity:.2e}")
@@ -400,6 +450,7 @@ def main():
                      "algorithmic_bytes_per_launch": per_launch},
         "cpu_baseline": cpu,
         "batched": batched,
+        "decode_step_tinyllama": tiny,
         "parity_max_rel_err": parity,
         "device": info["name"],
     }

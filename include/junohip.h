@@ -177,6 +177,14 @@ int jh_rope_kv_dev(float *q, const float *k, const float *v, int n_heads, int n_
 int jh_attention_dev(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,
                      int head_dim, const int *d_pos, int max_seq, float *out, void *stream);
 
+/* The attention sub-layer of one position in one launch pair: rope of the raw
+ * projections q and k at *d_pos, k and v appended to the caches, and the
+ * attention output (q is not modified).  transformerLayer :765-773 with rope
+ * :1657-1671 and gqa :1678-1731.  Same workspace as jh_attention_dev. */
+int jh_rope_attention_dev(const float *q, const float *k, const float *v, int n_heads, int n_kv_heads, int head_dim,
+                          const int *d_pos, int max_seq, float theta, float *k_cache, float *v_cache, float *out,
+                          void *stream);
+
 /* out = silu(gate) * up.  silu and ffn: LlamaTransformerHandler.java:1733-1735,
  * 796-797. */
 int jh_silu_mul_dev(const float *gate, const float *up, int n, float *out, void *stream);

@@ -42,6 +42,7 @@ SIGNATURES = {
     "jh_rmsnorm_dev": (_I, [_P, _P, _P, _I, ctypes.c_float, _P, _P, _P]),
     "jh_rope_kv_dev": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P]),
     "jh_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, _P, _P]),
+    "jh_rope_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _P]),
     "jh_silu_mul_dev": (_I, [_P, _P, _I, _P, _P]),
     "jh_pos_increment_dev": (_I, [_P, _I, _P]),
 }

@@ -587,7 +587,7 @@ static int check_heads(int n_heads, int n_kv_heads, int head_dim, int max_seq) {
         return fail(JH_EINVAL, "n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
     if (head_dim < 2 || head_dim % 2 || head_dim > 256)
         return fail(JH_EINVAL, "head_dim=%d must be even and in [2, 256]", head_dim);
-    if (max_seq < 1) return fail(JH_EINVAL, "max_seq=%d must be >= 1", max_seq);
+    if (max_seq < 1 || max_seq > 32768) return fail(JH_EINVAL, "max_seq=%d outside [1, 32768]", max_seq);
     return JH_OK;
 }
 
@@ -602,24 +602,36 @@ int jh_rope_kv_dev(float *q, const float *k, const float *v, int n_heads, int n_
     return ok();
 }
 
-int jh_attention_dev(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,
-                     int head_dim, const int *d_pos, int max_seq, float *out, void *stream) {
+static int attention_common(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
+                            int n_heads, int n_kv_heads, int head_dim, const int *d_pos, int max_seq, float theta,
+                            bool fused, float *out, void *stream) {
     int rc;
     if ((rc = check_heads(n_heads, n_kv_heads, head_dim, max_seq))) return rc;
-    if (!q || !k_cache || !v_cache || !d_pos || !out) return fail(JH_EINVAL, "pointers must not be null");
-    if (jh::attention_lds_bytes(n_heads, n_kv_heads, head_dim) > 160 * 1024)
-        return fail(JH_EUNSUPPORTED, "n_heads / n_kv_heads = %d too large for one workgroup's LDS",
-                    n_heads / n_kv_heads);
+    if (!q || !k_cache || !v_cache || !d_pos || !out || (fused && (!k_new || !v_new)))
+        return fail(JH_EINVAL, "pointers must not be null");
     int dev = 0;
     JH_HIP("hipGetDevice", hipGetDevice(&dev));
     void *ws = nullptr;
     if ((rc = stream_workspace(dev, (hipStream_t)stream, jh::attention_workspace_bytes(n_heads, head_dim, max_seq),
                                &ws)))
         return rc;
-    hipError_t e = jh::launch_attention(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos, max_seq, out, ws,
-                                        (hipStream_t)stream);
+    hipError_t e = jh::launch_attention(q, k_new, v_new, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos,
+                                        max_seq, theta, fused, out, ws, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail("attention launch", e);
     return ok();
+}
+
+int jh_attention_dev(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,
+                     int head_dim, const int *d_pos, int max_seq, float *out, void *stream) {
+    return attention_common(q, nullptr, nullptr, const_cast<float *>(k_cache), const_cast<float *>(v_cache), n_heads,
+                            n_kv_heads, head_dim, d_pos, max_seq, 0.f, false, out, stream);
+}
+
+int jh_rope_attention_dev(const float *q, const float *k, const float *v, int n_heads, int n_kv_heads, int head_dim,
+                          const int *d_pos, int max_seq, float theta, float *k_cache, float *v_cache, float *out,
+                          void *stream) {
+    return attention_common(q, k, v, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos, max_seq, theta, true, out,
+                            stream);
 }
 
 int jh_silu_mul_dev(const float *gate, const float *up, int n, float *out, void *stream) {

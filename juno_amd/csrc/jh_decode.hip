@@ -1,7 +1,7 @@
 // jh_decode.hip -- the rest of a Llama decode step on the device, around the
 // quantized GEMVs: RMS normalisation (fused with the residual add), rotary
-// embeddings fused with the KV-cache append, grouped-query attention over the
-// cache, and the SwiGLU product.  Each kernel restates one method of
+// embeddings with the KV-cache append (alone, or fused into attention),
+// grouped-query attention over the cache, and the SwiGLU product.  Each kernel restates one method of
 // LlamaTransformerHandler (citations per kernel) with the reference's
 // precision choices: fp32 data, double where the reference computes in double
 // (the rsqrt argument, rope's frequency / angle / cos / sin, softmax's and
@@ -84,90 +84,131 @@ __global__ __launch_bounds__(256) void rope_kv_k(float *__restrict__ q, const fl
 
 // ------------------------------------------------------------------ gqa
 // gqa, LlamaTransformerHandler.java:1678-1715, with softmax :1718-1731.
-// Split over the sequence: workgroup (g, c) takes KV head g and positions
-// [c*TC, c*TC + TC) for all R = n_heads / n_kv_heads query heads of g, with
-// the chunk's K and V staged in LDS once.  It writes, per query head, the
-// chunk's max score m, sum of exp(s - m) l, and sum of exp(s - m) v; the
-// combine kernel rescales the chunks to the global max and normalises.
-// Each dot product q . k runs over d in order, as the reference's does.
-__global__ __launch_bounds__(256) void attn_chunk_k(const float *__restrict__ q, const float *__restrict__ k_cache,
-                                                    const float *__restrict__ v_cache, int n_heads, int n_kv_heads,
-                                                    int head_dim, const int *__restrict__ d_pos, int max_seq,
-                                                    int tc, float scale, float *__restrict__ part) {
+// Split over the sequence: one wavefront per (query head h, chunk c of 64
+// positions; 32 for head_dim > 128).  The chunk's K and V rows are staged in
+// LDS with coalesced 16-byte loads; then one position per lane for the
+// scores and one output dimension per lane (per 64) for the weighted V sum.
+// It writes the chunk's max score m, sum of exp(s - m) l and sum of
+// exp(s - m) v; attn_combine_k rescales the chunks to the global max and
+// normalises.  Each dot product q . k runs over d in order, as the reference's.
+//
+// FUSED: q, k, v are the raw projections of this position; the kernel applies
+// rope (:765-766) to q (per wavefront) and k, and the wavefronts whose chunk
+// holds the position append rotated k and v to the cache (:769-770; the R
+// wavefronts of a KV head write identical values) and use them from LDS.
+__device__ __forceinline__ void rope_pair(float &x0, float &x1, int p, int head_dim, int pos, float theta) {
+    const double freq = 1.0 / pow((double)theta, (2.0 * p) / head_dim);
+    const double angle = pos * freq;
+    const float c = (float)cos(angle), s = (float)sin(angle);
+    const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+    x0 = y0;
+    x1 = y1;
+}
+
+// chunk length: one position per lane, fewer for wide heads (LDS holds the
+// chunk's K and V)
+__host__ __device__ constexpr int attn_tc(int head_dim) { return head_dim <= 128 ? 64 : 32; }
+
+template <bool FUSED>
+__global__ __launch_bounds__(64) void attn_chunk_k(const float *__restrict__ q, const float *__restrict__ k_new,
+                                                   const float *__restrict__ v_new, float *__restrict__ k_cache,
+                                                   float *__restrict__ v_cache, int n_heads, int n_kv_heads,
+                                                   int head_dim, const int *__restrict__ d_pos, int max_seq,
+                                                   float theta, float scale, float *__restrict__ part) {
     extern __shared__ float lds[];
-    const int T = min(*d_pos, max_seq - 1) + 1;
-    const int g = blockIdx.x, c = blockIdx.y, t0 = c * tc;
-    if (t0 >= T) return;  // uniform across the workgroup
-    const int R = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim, nt = min(tc, T - t0);
-    const int kst = head_dim + 1;  // padded K rows: consecutive positions in different banks
-    float *sk = lds;                        // [tc][head_dim + 1]
-    float *sv = sk + tc * kst;              // [tc][head_dim]
-    float *sq = sv + tc * head_dim;         // [R][head_dim]
-    float *sp = sq + R * head_dim;          // [R][tc]
-    float *sm = sp + R * tc;                // [R] max, [R] sum
-    for (int i = threadIdx.x; i < nt * head_dim; i += 256) {
-        const int t = i / head_dim, d = i % head_dim;
+    const int tc = attn_tc(head_dim), kst = head_dim + 1;  // padded K rows: lane t in its own bank
+    float *sk = lds;                  // [tc][head_dim + 1]
+    float *sv = sk + tc * kst;        // [tc][head_dim]
+    float *sq = sv + tc * head_dim;   // [head_dim]
+    float *sp = sq + head_dim;        // [tc]
+    const int pos = min(*d_pos, max_seq - 1), T = pos + 1;
+    const int h = blockIdx.x, c = blockIdx.y, t0 = c * tc, lane = threadIdx.x;
+    if (t0 >= T) return;  // uniform across the wavefront
+    const int R = n_heads / n_kv_heads, g = h / R, kv_dim = n_kv_heads * head_dim;
+    const int nt = min(tc, T - t0);
+    const bool has_pos = FUSED && pos < t0 + tc;  // this chunk holds the new position
+    // the chunk's K and V rows (cache positions; the new one is overwritten below)
+    const int q4 = head_dim / 4, n4 = nt * q4;
+    for (int i = lane; i < n4; i += 64) {
+        const int t = i / q4, d = 4 * (i % q4);
         const size_t o = (size_t)(t0 + t) * kv_dim + g * head_dim + d;
-        sk[t * kst + d] = k_cache[o];
-        sv[t * head_dim + d] = v_cache[o];
+        const float4 kk = *reinterpret_cast<const float4 *>(k_cache + o);
+        const float4 vv = *reinterpret_cast<const float4 *>(v_cache + o);
+        float *kd = sk + t * kst + d;
+        kd[0] = kk.x; kd[1] = kk.y; kd[2] = kk.z; kd[3] = kk.w;
+        *reinterpret_cast<float4 *>(sv + t * head_dim + d) = vv;
     }
-    for (int i = threadIdx.x; i < R * head_dim; i += 256) sq[i] = q[g * R * head_dim + i];
     __syncthreads();
-    for (int i = threadIdx.x; i < R * nt; i += 256) {
-        const int j = i / nt, t = i % nt;
+    for (int p = lane; p < head_dim / 2; p += 64) {
+        float a = q[h * head_dim + 2 * p], b = q[h * head_dim + 2 * p + 1];
+        if (FUSED) rope_pair(a, b, p, head_dim, pos, theta);
+        sq[2 * p] = a;
+        sq[2 * p + 1] = b;
+        if (has_pos) {
+            float ka = k_new[g * head_dim + 2 * p], kb = k_new[g * head_dim + 2 * p + 1];
+            rope_pair(ka, kb, p, head_dim, pos, theta);
+            const int tp = pos - t0;
+            sk[tp * kst + 2 * p] = ka;
+            sk[tp * kst + 2 * p + 1] = kb;
+            const size_t o = (size_t)pos * kv_dim + g * head_dim + 2 * p;
+            k_cache[o] = ka;
+            k_cache[o + 1] = kb;
+        }
+    }
+    if (has_pos)
+        for (int d = lane; d < head_dim; d += 64) {
+            const float v = v_new[g * head_dim + d];
+            sv[(pos - t0) * head_dim + d] = v;
+            v_cache[(size_t)pos * kv_dim + g * head_dim + d] = v;
+        }
+    __syncthreads();
+    float s = -INFINITY;
+    if (lane < nt) {
         float dot = 0.f;
-        for (int d = 0; d < head_dim; d++) dot += sq[j * head_dim + d] * sk[t * kst + d];
-        sp[j * tc + t] = dot * scale;
+        for (int d = 0; d < head_dim; d++) dot += sq[d] * sk[lane * kst + d];
+        s = dot * scale;
     }
-    __syncthreads();
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int j = wave; j < R; j += 4) {
-        float m = -INFINITY;
-        for (int t = lane; t < nt; t += 64) m = fmaxf(m, sp[j * tc + t]);
+    float m = s;
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-        float l = 0.f;
-        for (int t = lane; t < nt; t += 64) {
-            const float e = (float)exp((double)(sp[j * tc + t] - m));
-            sp[j * tc + t] = e;
-            l += e;
-        }
-        l = wave_sum(l);
-        if (lane == 0) {
-            sm[j] = m;
-            sm[R + j] = l;
-        }
-    }
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float e = lane < nt ? (float)exp((double)(s - m)) : 0.f;
+    const float l = wave_sum(e);
+    if (lane < tc) sp[lane] = e;
     __syncthreads();
-    const int nch = gridDim.y;
-    for (int i = threadIdx.x; i < R * head_dim; i += 256) {
-        const int j = i / head_dim, d = i % head_dim;
+    float *ph = part + ((size_t)h * gridDim.y + c) * (head_dim + 2);
+    for (int d = lane; d < head_dim; d += 64) {
         float o = 0.f;
-        for (int t = 0; t < nt; t++) o += sp[j * tc + t] * sv[t * head_dim + d];
-        const int h = g * R + j;
-        part[((size_t)h * nch + c) * (head_dim + 2) + 2 + d] = o;
+        for (int t = 0; t < nt; t++) o += sp[t] * sv[t * head_dim + d];
+        ph[2 + d] = o;
     }
-    if (threadIdx.x < R) {
-        const int h = g * R + threadIdx.x;
-        part[((size_t)h * nch + c) * (head_dim + 2)] = sm[threadIdx.x];
-        part[((size_t)h * nch + c) * (head_dim + 2) + 1] = sm[R + threadIdx.x];
+    if (lane == 0) {
+        ph[0] = m;
+        ph[1] = l;
     }
 }
 
 __global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ part, int head_dim,
-                                                      const int *__restrict__ d_pos, int max_seq, int tc, int nchmax,
+                                                      const int *__restrict__ d_pos, int max_seq, int nchmax,
                                                       float *__restrict__ out) {
-    const int h = blockIdx.x;
-    const int T = min(*d_pos, max_seq - 1) + 1, nch = (T + tc - 1) / tc;
+    __shared__ float wc[1024];
+    __shared__ float sL;
+    const int h = blockIdx.x, tc = attn_tc(head_dim);
+    const int T = min(*d_pos, max_seq - 1) + 1, nch = min((T + tc - 1) / tc, 1024);
     const float *ph = part + (size_t)h * nchmax * (head_dim + 2);
     float M = -INFINITY;
     for (int c = 0; c < nch; c++) M = fmaxf(M, ph[c * (head_dim + 2)]);
-    float L = 0.f;
-    for (int c = 0; c < nch; c++) L += ph[c * (head_dim + 2) + 1] * (float)exp((double)(ph[c * (head_dim + 2)] - M));
+    for (int c = threadIdx.x; c < nch; c += 256) wc[c] = (float)exp((double)(ph[c * (head_dim + 2)] - M));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float L = 0.f;
+        for (int c = 0; c < nch; c++) L += ph[c * (head_dim + 2) + 1] * wc[c];
+        sL = L;
+    }
+    __syncthreads();
+    const float L = sL;
     for (int d = threadIdx.x; d < head_dim; d += 256) {
         float o = 0.f;
-        for (int c = 0; c < nch; c++)
-            o += ph[c * (head_dim + 2) + 2 + d] * (float)exp((double)(ph[c * (head_dim + 2)] - M));
+        for (int c = 0; c < nch; c++) o += ph[c * (head_dim + 2) + 2 + d] * wc[c];
         out[(size_t)h * head_dim + d] = o / L;
     }
 }
@@ -204,34 +245,36 @@ hipError_t launch_rope_kv(float *q, const float *k, const float *v, int n_heads,
     return hipGetLastError();
 }
 
-int attention_chunk(int head_dim) { return head_dim >= 256 ? 32 : 8192 / head_dim; }
-
 size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq) {
-    const int tc = attention_chunk(head_dim), nch = (max_seq + tc - 1) / tc;
+    const int nch = (max_seq + attn_tc(head_dim) - 1) / attn_tc(head_dim);
     return (size_t)n_heads * nch * (head_dim + 2) * sizeof(float);
 }
 
-size_t attention_lds_bytes(int n_heads, int n_kv_heads, int head_dim) {
-    const int tc = attention_chunk(head_dim), R = n_heads / n_kv_heads;
-    return sizeof(float) * ((size_t)tc * (head_dim + 1) + (size_t)tc * head_dim + (size_t)R * head_dim +
-                            (size_t)R * tc + 2 * (size_t)R);
-}
-
-hipError_t launch_attention(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,
-                            int head_dim, const int *d_pos, int max_seq, float *out, void *workspace,
-                            hipStream_t s) {
-    const int tc = attention_chunk(head_dim), nch = (max_seq + tc - 1) / tc;
-    const size_t lds = attention_lds_bytes(n_heads, n_kv_heads, head_dim);
-    static bool attr = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_chunk_k),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
-    (void)attr;
+hipError_t launch_attention(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
+                            int n_heads, int n_kv_heads, int head_dim, const int *d_pos, int max_seq, float theta,
+                            bool fused, float *out, void *workspace, hipStream_t s) {
+    const int tc = attn_tc(head_dim), nch = (max_seq + tc - 1) / tc;
+    if (nch > 1024) return hipErrorNotSupported;  // combine weights live in a fixed LDS array
     const float scale = (float)(1.0 / sqrt((double)head_dim));
     float *part = static_cast<float *>(workspace);
-    attn_chunk_k<<<dim3(n_kv_heads, nch), 256, lds, s>>>(q, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos,
-                                                         max_seq, tc, scale, part);
+    const dim3 grid(n_heads, nch);
+    const size_t lds = sizeof(float) * ((size_t)tc * (head_dim + 1) + (size_t)tc * head_dim + head_dim + tc);
+    static const bool attr = [] {
+        bool ok = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_chunk_k<true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+        return ok && hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_chunk_k<false>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    }();
+    (void)attr;
+    if (fused)
+        attn_chunk_k<true><<<grid, 64, lds, s>>>(q, k_new, v_new, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos,
+                                                max_seq, theta, scale, part);
+    else
+        attn_chunk_k<false><<<grid, 64, lds, s>>>(q, nullptr, nullptr, k_cache, v_cache, n_heads, n_kv_heads, head_dim,
+                                                 d_pos, max_seq, theta, scale, part);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attn_combine_k<<<n_heads, 256, 0, s>>>(part, head_dim, d_pos, max_seq, tc, nch, out);
+    attn_combine_k<<<n_heads, 256, 0, s>>>(part, head_dim, d_pos, max_seq, nch, out);
     return hipGetLastError();
 }
 

@@ -75,9 +75,11 @@ hipError_t launch_rmsnorm(const float *x, const float *res, const float *w, int 
 hipError_t launch_rope_kv(float *q, const float *k, const float *v, int n_heads, int n_kv_heads, int head_dim,
                           const int *d_pos, int max_seq, float theta, float *k_cache, float *v_cache, hipStream_t s);
 size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq);
-size_t attention_lds_bytes(int n_heads, int n_kv_heads, int head_dim);
-hipError_t launch_attention(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,
-                            int head_dim, const int *d_pos, int max_seq, float *out, void *workspace, hipStream_t s);
+// fused: q, k_new, v_new are this position's raw projections (rope + append
+// inside); otherwise q is rotated and the cache already holds the position
+hipError_t launch_attention(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
+                            int n_heads, int n_kv_heads, int head_dim, const int *d_pos, int max_seq, float theta,
+                            bool fused, float *out, void *workspace, hipStream_t s);
 hipError_t launch_silu_mul(const float *gate, const float *up, int n, float *out, hipStream_t s);
 hipError_t launch_pos_increment(int *d_pos, int delta, hipStream_t s);
 

@@ -195,10 +195,9 @@ class LlamaDecoder:
                 _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(lw.attn_norm), H, eps, P(self.x), P(self.xn), s))
             m = lw.mats
             self._group([m["q"], m["k"], m["v"]], [self.xn] * 3, [self.q, self.k, self.v], s)
-            _check(L.jh_rope_kv_dev(P(self.q), P(self.k), P(self.v), nh, nkv, hd, P(self.pos), self.max_seq,
-                                    c.rope_theta, P(self.k_cache[li]), P(self.v_cache[li]), s))
-            _check(L.jh_attention_dev(P(self.q), P(self.k_cache[li]), P(self.v_cache[li]), nh, nkv, hd, P(self.pos),
-                                      self.max_seq, P(self.att), s))
+            # rope on q and k, KV append and gqa (:765-773) in one launch pair
+            _check(L.jh_rope_attention_dev(P(self.q), P(self.k), P(self.v), nh, nkv, hd, P(self.pos), self.max_seq,
+                                           c.rope_theta, P(self.k_cache[li]), P(self.v_cache[li]), P(self.att), s))
             self._group([m["o"]], [self.att], [self.proj], s)
             # x2 = x + attnProj (:778); rmsNorm(x2) (:781)
             _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(lw.ffn_norm), H, eps, P(self.x), P(self.xn), s))

@@ -110,6 +110,32 @@ def test_attention(L, nh, nkv, hd, T):
         assert np.array_equal(got.reshape(nh, hd), np.repeat(vc[0].reshape(nkv, hd), nh // nkv, axis=0))
 
 
+@pytest.mark.parametrize("nh,nkv,hd,pos", [(32, 4, 64, 0), (32, 4, 64, 63), (32, 4, 64, 64), (32, 4, 64, 511),
+                                           (32, 8, 128, 200), (4, 1, 256, 70)])
+def test_rope_attention_fused(L, nh, nkv, hd, pos):
+    """rope of q and k, KV append and gqa in one call == the oracle's three steps."""
+    say("rope_attention", nh, nkv, hd, pos)
+    max_seq, theta, kvd = 600, 10000.0, nkv * hd
+    q, k, v = vec(nh * hd, pos + 1), vec(kvd, pos + 2), vec(kvd, pos + 3)
+    kc = vec(max_seq * kvd, pos + 4).reshape(max_seq, kvd)
+    vc = vec(max_seq * kvd, pos + 5).reshape(max_seq, kvd)
+    dkc, dvc, dq = dev(kc), dev(vc), dev(q)
+    out = torch.full((nh * hd,), float("nan"), device="cuda")
+    dpos = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    assert L.jh_rope_attention_dev(P(dq), P(dev(k)), P(dev(v)), nh, nkv, hd, P(dpos), max_seq, theta, P(dkc), P(dvc),
+                                   P(out), None) == 0
+    kc_ref, vc_ref = kc.copy(), vc.copy()
+    kc_ref[pos] = O.rope(k, pos, nkv, hd, theta)
+    vc_ref[pos] = v
+    ref = O.gqa(O.rope(q, pos, nh, hd, theta), kc_ref, vc_ref, nh, nkv, hd, pos + 1)
+    got = out.cpu().numpy()
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max() + 1e-7
+    assert np.allclose(dkc[pos].cpu().numpy(), kc_ref[pos], rtol=2e-6, atol=2e-6)
+    assert np.array_equal(dvc[pos].cpu().numpy(), v)
+    assert np.array_equal(np.delete(dkc.cpu().numpy(), pos, 0), np.delete(kc, pos, 0))
+    assert np.array_equal(dq.cpu().numpy(), q)  # q itself is not modified
+
+
 def test_attention_arguments(L):
     d = torch.zeros(64, device="cuda")
     pos = torch.zeros(1, dtype=torch.int32, device="cuda")
