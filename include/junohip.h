@@ -25,7 +25,7 @@
  *   - Weight matrices are W[rows][cols] row-major in GGUF packed blocks along
  *     cols, exactly the bytes of GgufReader.QuantizedTensor.data()
  *     (GgufReader.java:319-339).  Supported ggml types: 0 (F32), 8 (Q8_0),
- *     12 (Q4_K), 14 (Q6_K).
+ *     12 (Q4_K), 13 (Q5_K), 14 (Q6_K).
  *   - Host-pointer entry points are synchronous and thread-safe: each host
  *     thread has its own HIP stream and staging buffers per device.
  *   - Device-pointer entry points (*_dev) enqueue on the given stream
@@ -55,6 +55,7 @@ enum {
     JH_TYPE_F32 = 0,
     JH_TYPE_Q8_0 = 8,
     JH_TYPE_Q4_K = 12,
+    JH_TYPE_Q5_K = 13,
     JH_TYPE_Q6_K = 14,
 };
 

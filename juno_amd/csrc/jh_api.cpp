@@ -93,6 +93,7 @@ bool type_geometry(int type, int *qk, int *bb) {
     case JH_TYPE_F32: *qk = 1; *bb = 4; return true;
     case JH_TYPE_Q8_0: *qk = 32; *bb = 34; return true;
     case JH_TYPE_Q4_K: *qk = 256; *bb = 144; return true;
+    case JH_TYPE_Q5_K: *qk = 256; *bb = 176; return true;
     case JH_TYPE_Q6_K: *qk = 256; *bb = 210; return true;
     default: return false;
     }

@@ -20,11 +20,13 @@
 
 namespace jh {
 
-// ---------------------------------------------------------------- Q4_K
+// ---------------------------------------------------------------- Q4_K / Q5_K
 // Lane (kb, ch): block b = step*8 + kb, 16-byte qs chunk ch of that block.
 // Chunk ch covers group g = ch/2, elements 16*(ch&1) .. +16 of sub-block 2g
-// (low nibbles) and of sub-block 2g+1 (high nibbles).
-template <int R, int B>
+// (low nibbles) and of sub-block 2g+1 (high nibbles).  Q5_K (Q5 = true,
+// matVecQ5Kraw, LlamaTransformerHandler.java:1525-1576) adds the 5th bits:
+// bit 2g / 2g+1 of qh[l] for the same 16 elements l.
+template <int R, int B, bool Q5 = false>
 __device__ __forceinline__ void gemv_q4k_body(int wg, const uint8_t *__restrict__ W, size_t pitch, int nb,
                                                 int nrows, const float *__restrict__ X, int ldx,
                                                 float *__restrict__ Y, int ldy) {
@@ -43,13 +45,15 @@ __device__ __forceinline__ void gemv_q4k_body(int wg, const uint8_t *__restrict_
 #pragma unroll
     for (int i = 0; i < R; i++) rowp[i] = W + (size_t)min(r0 + i, nrows - 1) * pitch;
 
+    constexpr int kBB = Q5 ? 176 : 144, kQs = Q5 ? 48 : 16;
     for (int b = kb; b < nb; b += 8) {
-        uint4 hdr[R], qs[R];
+        uint4 hdr[R], qs[R], qh[R];
 #pragma unroll
         for (int i = 0; i < R; i++) {
-            const uint8_t *bp = rowp[i] + (size_t)b * 144;
+            const uint8_t *bp = rowp[i] + (size_t)b * kBB;
             hdr[i] = *reinterpret_cast<const uint4 *>(bp);
-            qs[i] = load_stream16(bp + 16 + ch * 16);
+            qs[i] = load_stream16(bp + kQs + ch * 16);
+            if (Q5) qh[i] = *reinterpret_cast<const uint4 *>(bp + 16 + hf * 16);
         }
         const int xo = b * 256 + g * 64 + hf * 16;
         float xl[B][16], xh[B][16], sl[B], sh[B];
@@ -77,12 +81,17 @@ __device__ __forceinline__ void gemv_q4k_body(int wg, const uint8_t *__restrict_
             const float sc0 = d * (float)ls0, mn0 = dmin * (float)lm0;
             const float sc1 = d * (float)ls1, mn1 = dmin * (float)lm1;
             const uint32_t w[4] = {qs[i].x, qs[i].y, qs[i].z, qs[i].w};
+            const uint32_t h5[4] = {qh[i].x, qh[i].y, qh[i].z, qh[i].w};
 #pragma unroll
             for (int j = 0; j < B; j++) {
                 float dl = 0.f, dh = 0.f;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const uint32_t lo = w[k] & 0x0F0F0F0Fu, hi = (w[k] >> 4) & 0x0F0F0F0Fu;
+                    uint32_t lo = w[k] & 0x0F0F0F0Fu, hi = (w[k] >> 4) & 0x0F0F0F0Fu;
+                    if (Q5) {
+                        lo |= ((h5[k] >> (2 * g)) & 0x01010101u) << 4;
+                        hi |= ((h5[k] >> (2 * g + 1)) & 0x01010101u) << 4;
+                    }
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         dl = fmaf((float)byte_of(lo, e), xl[j][4 * k + e], dl);
@@ -289,6 +298,11 @@ __global__ __launch_bounds__(256) void gemv_q4k(const uint8_t *__restrict__ W, s
     gemv_q4k_body<R, B>(blockIdx.x, W, pitch, nb, nrows, X, ldx, Y, ldy);
 }
 template <int R, int B>
+__global__ __launch_bounds__(256) void gemv_q5k(const uint8_t *__restrict__ W, size_t pitch, int nb, int nrows,
+                                                const float *__restrict__ X, int ldx, float *__restrict__ Y, int ldy) {
+    gemv_q4k_body<R, B, true>(blockIdx.x, W, pitch, nb, nrows, X, ldx, Y, ldy);
+}
+template <int R, int B>
 __global__ __launch_bounds__(256) void gemv_q6k(const uint8_t *__restrict__ W, size_t pitch, int nb, int nrows,
                                                 const float *__restrict__ X, int ldx, float *__restrict__ Y, int ldy) {
     gemv_q6k_body<R, B>(blockIdx.x, W, pitch, nb, nrows, X, ldx, Y, ldy);
@@ -315,12 +329,14 @@ __global__ __launch_bounds__(256) void gemv_group(GroupArgs g) {
     if (q.rows_per_wave == 2) {
         switch (q.type) {
         case 12: gemv_q4k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
+        case 13: gemv_q4k_body<2, 1, true>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         case 14: gemv_q6k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         default: gemv_q8_0_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         }
     } else {
         switch (q.type) {
         case 12: gemv_q4k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
+        case 13: gemv_q4k_body<1, 1, true>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         case 14: gemv_q6k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         default: gemv_q8_0_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         }
@@ -331,7 +347,7 @@ hipError_t launch_gemv_group(GroupArgs g, hipStream_t s) {
     int total = 0;
     for (int i = 0; i < g.n; i++) {
         GroupProblem &q = g.p[i];
-        if (q.type != 12 && q.type != 14 && q.type != 8) return hipErrorInvalidValue;
+        if (q.type != 12 && q.type != 13 && q.type != 14 && q.type != 8) return hipErrorInvalidValue;
         q.rows_per_wave = q.nrows >= 2048 ? 2 : 1;
         q.wg_begin = total;
         total += (q.nrows + 4 * q.rows_per_wave - 1) / (4 * q.rows_per_wave);
@@ -375,6 +391,7 @@ static hipError_t launch_q(int type, const uint8_t *W, size_t pitch, int nb, int
     dim3 grid((nrows + rows_per_wg - 1) / rows_per_wg), block(256);
     switch (type) {
     case 12: gemv_q4k<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
+    case 13: gemv_q5k<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
     case 14: gemv_q6k<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
     case 8: gemv_q8_0<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
     default: return hipErrorInvalidValue;

@@ -222,6 +222,7 @@ __device__ __forceinline__ float limbs(int h, int m, int l) {
 // blocks per wave tile, max 16-byte chunks of one row tile in LDS.
 template <int T> struct Fmt;
 template <> struct Fmt<12> { static constexpr int QK = 256, BB = 144, LPB = 4, TBMAX = 16, CH = 145; };
+template <> struct Fmt<13> { static constexpr int QK = 256, BB = 176, LPB = 4, TBMAX = 16, CH = 177; };
 template <> struct Fmt<14> { static constexpr int QK = 256, BB = 210, LPB = 4, TBMAX = 16, CH = 212; };
 template <> struct Fmt<8> { static constexpr int QK = 32, BB = 34, LPB = 1, TBMAX = 64, CH = 138; };
 
@@ -272,6 +273,9 @@ template <> struct XRegs<12> : XLimbs<16> {
         xs1 = act ? s1 : 0.f;
     }
 };
+
+// Q5_K: the same columns as Q4_K
+template <> struct XRegs<13> : XRegs<12> {};
 
 // Q6_K: runs k = 0..3 of 16 columns b*256 + hh*128 + 32k + l0 (hh = g/2, l0 = 16(g&1))
 template <> struct XRegs<14> : XLimbs<16> {
@@ -332,15 +336,31 @@ template <> struct XRegs<8> : XLimbs<8> {
 // Dot product of one block slot of one row (block bytes at LDS byte address p).
 // Q4_K (LlamaTransformerHandler.java:1428-1468): sum over sub-blocks 2g, 2g+1 of
 //   d*ls*sum(q*x) - dmin*lm*sum(x).
-__device__ __forceinline__ float block_dot(const XRegs<12> &x, const uint8_t *p, int g) {
+// Q5_K (Q5 = true, :1525-1576): the same with qs at +48 and q's 5th bit from
+// qh (+16): bit 2g / 2g+1 of qh[l].
+template <bool Q5>
+__device__ __forceinline__ float kq_block_dot(const XRegs<12> &x, const uint8_t *p, int g) {
+    constexpr int kQs = Q5 ? 48 : 16;
     const uint4 hd = *reinterpret_cast<const uint4 *>(p);
-    const uint4 qa = *reinterpret_cast<const uint4 *>(p + 16 + 32 * g);
-    const uint4 qb = *reinterpret_cast<const uint4 *>(p + 32 + 32 * g);
+    const uint4 qa = *reinterpret_cast<const uint4 *>(p + kQs + 32 * g);
+    const uint4 qb = *reinterpret_cast<const uint4 *>(p + kQs + 16 + 32 * g);
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    uint32_t q5[8] = {};
+    if (Q5) {
+        const uint4 ha = *reinterpret_cast<const uint4 *>(p + 16);
+        const uint4 hb = *reinterpret_cast<const uint4 *>(p + 32);
+        const uint32_t h[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+#pragma unroll
+        for (int k = 0; k < 8; k++) q5[k] = h[k] >> (2 * g);
+    }
     int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        const uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+        uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+        if (Q5) {
+            lo |= (q5[k] & 0x01010101u) << 4;
+            hi |= ((q5[k] >> 1) & 0x01010101u) << 4;
+        }
         h0 = sdot4(lo, x.h[k], h0);
         m0 = udot4(lo, x.m[k], m0);
         l0 = udot4(lo, x.l[k], l0);
@@ -362,6 +382,12 @@ __device__ __forceinline__ float block_dot(const XRegs<12> &x, const uint8_t *p,
     const float mn = fmaf((float)lm1, x.xs1, (float)lm0 * x.xs0);
     const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
     return fmaf(d * x.a, t, -dmin * mn);
+}
+__device__ __forceinline__ float block_dot(const XRegs<12> &x, const uint8_t *p, int g) {
+    return kq_block_dot<false>(x, p, g);
+}
+__device__ __forceinline__ float block_dot(const XRegs<13> &x, const uint8_t *p, int g) {
+    return kq_block_dot<true>(x, p, g);
 }
 
 // Q6_K (LlamaTransformerHandler.java:1587-1638): lane g covers half hh = g/2 and
@@ -637,6 +663,7 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
 bool staged_supported(int type, int cols) {
     switch (type) {
     case 12: return cols % 256 == 0 && cols / 256 <= 4 * Fmt<12>::TBMAX;
+    case 13: return cols % 256 == 0 && cols / 256 <= 4 * Fmt<13>::TBMAX;
     case 14: return cols % 256 == 0 && cols / 256 <= 4 * Fmt<14>::TBMAX;
     case 8: return cols % 32 == 0 && cols / 32 <= 4 * Fmt<8>::TBMAX;
     default: return false;
@@ -666,6 +693,7 @@ static hipError_t launch_staged_any(const StagedArgs &sa, int type, hipStream_t 
     const int R = staged_rows(2);
     switch (type) {
     case 12: return launch_staged_r<12>(sa, R, s);
+    case 13: return launch_staged_r<13>(sa, R, s);
     case 14: return launch_staged_r<14>(sa, R, s);
     case 8: return launch_staged_r<8>(sa, R, s);
     default: return hipErrorNotSupported;

@@ -1,4 +1,4 @@
-// jh_mfma.hip -- batched decode (16 <= B <= 64) on Q4_K / Q6_K / Q8_0 through
+// jh_mfma.hip -- batched decode (16 <= B <= 64) on Q4_K / Q5_K / Q6_K / Q8_0 through
 // LDS + fp16 MFMA.
 //
 // Y[b][r] = sum_c deq(W[r][c]) * X[b][c] is a dense contraction once B >= 16:
@@ -193,20 +193,30 @@ __device__ __forceinline__ void col_terms(const Ctx &c, int n, float (&S)[16], f
 // B = 1024 + ls*q (<= 1969, exact), built with one 24-bit multiply-add per
 // pair; 1024 * sum(x) and the min term (one more MFMA: A = [sub-block sums
 // hi | lo], B = [lm | lm]) are removed per super-block with d and dmin.
-struct FmtQ4K {
-    static constexpr int kBytes = 144;
-    static constexpr int kChunks = 9;  // rows are 16-byte aligned (pitch 144 * n, aligned base)
+// Q5_K (Q5 = true, matVecQ5Kraw :1525-1576): q has a 5th bit from qh, so
+// ls*q reaches 1953 and 1024 + ls*q would pass fp16's exact integers; B =
+// ls*q is converted instead (v_cvt_f16_u16, exact below 2048).
+template <bool Q5>
+struct FmtKQ {
+    static constexpr int kBytes = Q5 ? 176 : 144;
+    static constexpr int kChunks = kBytes / 16;  // rows are 16-byte aligned (pitch kBytes * n, aligned base)
+    static constexpr int kQs = Q5 ? 48 : 16;
     static constexpr bool kSums = true;
     struct Regs {
         u32x4 hd;
         u32x2 qp[4][2];
+        u32x2 qh[2];  // Q5_K: qh bytes 16 j + 8 kh .. +8 (bit s for sub-block s)
     };
     static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
         r.hd = *reinterpret_cast<const u32x4 *>(p);
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            r.qp[g][0] = *reinterpret_cast<const u32x2 *>(p + 16 + 32 * g + 8 * kh);
-            r.qp[g][1] = *reinterpret_cast<const u32x2 *>(p + 16 + 32 * g + 16 + 8 * kh);
+            r.qp[g][0] = *reinterpret_cast<const u32x2 *>(p + kQs + 32 * g + 8 * kh);
+            r.qp[g][1] = *reinterpret_cast<const u32x2 *>(p + kQs + 32 * g + 16 + 8 * kh);
+        }
+        if (Q5) {
+            r.qh[0] = *reinterpret_cast<const u32x2 *>(p + 16 + 8 * kh);
+            r.qh[1] = *reinterpret_cast<const u32x2 *>(p + 32 + 8 * kh);
         }
     }
     template <int NT>
@@ -228,8 +238,13 @@ struct FmtQ4K {
             // sub-block s = t/2: low nibbles of qs group s/2 for even s, high for odd
             const int s = t >> 1, g = s >> 1, hiN = s & 1;
             const u32x2 q = r.qp[g][t & 1];
-            const uint32_t nib0 = hiN ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
-            const uint32_t nib1 = hiN ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+            uint32_t nib0 = hiN ? (q.x >> 4) & 0x0F0F0F0Fu : q.x & 0x0F0F0F0Fu;
+            uint32_t nib1 = hiN ? (q.y >> 4) & 0x0F0F0F0Fu : q.y & 0x0F0F0F0Fu;
+            if (Q5) {
+                const u32x2 h = r.qh[t & 1];
+                nib0 |= ((h.x >> s) & 0x01010101u) << 4;
+                nib1 |= ((h.y >> s) & 0x01010101u) << 4;
+            }
             const uint32_t pr[4] = {__builtin_amdgcn_perm(0u, nib0, 0x0C010C00u),
                                     __builtin_amdgcn_perm(0u, nib0, 0x0C030C02u),
                                     __builtin_amdgcn_perm(0u, nib1, 0x0C010C00u),
@@ -237,9 +252,15 @@ struct FmtQ4K {
             half8 w;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const uint32_t v = __umul24(pr[j], (uint32_t)ls[s]) + 0x64006400u;
-                w[2 * j] = __builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF));
-                w[2 * j + 1] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+                if (Q5) {
+                    const uint32_t v = __umul24(pr[j], (uint32_t)ls[s]);  // two 16-bit products <= 1953
+                    w[2 * j] = (_Float16)(uint16_t)(v & 0xFFFF);
+                    w[2 * j + 1] = (_Float16)(uint16_t)(v >> 16);
+                } else {
+                    const uint32_t v = __umul24(pr[j], (uint32_t)ls[s]) + 0x64006400u;
+                    w[2 * j] = __builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF));
+                    w[2 * j + 1] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+                }
             }
             mfma_xw<NT>(c, w, 16 * t + 8 * c.kh, acc);
         }
@@ -256,10 +277,13 @@ struct FmtQ4K {
             col_terms<NT>(c, n, S, cs);
 #pragma unroll
             for (int i = 0; i < 16; i++)
-                tot[n][i] = fmaf(cs[i], fmaf(d, fmaf(-1024.f, S[i], acc[n][i]), -dmin * mn[i]), tot[n][i]);
+                tot[n][i] = fmaf(cs[i], fmaf(d, fmaf(Q5 ? 0.f : -1024.f, S[i], acc[n][i]), -dmin * mn[i]), tot[n][i]);
         }
     }
 };
+
+using FmtQ4K = FmtKQ<false>;
+using FmtQ5K = FmtKQ<true>;
 
 // Q6_K (matVecQ6Kraw, LlamaTransformerHandler.java:1587-1638): w = (d*sc_j)*(u - 32)
 // with u = 4 bits of ql | 2 bits of qh.  A 16-column sub-block is exactly one
@@ -516,7 +540,7 @@ static void mfma_split(int nrows, int nsb, int &tiles, int &ksplit, int &ksb) {
 }
 
 size_t mfma_workspace_bytes(int type, int B, int cols, int rows) {
-    if ((type != 12 && type != 14 && type != 8) || B < 16 || B > 64 || cols % 256 || rows < 1) return 0;
+    if ((type != 12 && type != 13 && type != 14 && type != 8) || B < 16 || B > 64 || cols % 256 || rows < 1) return 0;
     int tiles, ksplit, ksb;
     mfma_split(rows, cols / 256, tiles, ksplit, ksb);
     XWork w{(B + 31) / 32 * 32, cols, cols / 256, rows, ksplit, nullptr};
@@ -524,10 +548,10 @@ size_t mfma_workspace_bytes(int type, int B, int cols, int rows) {
 }
 
 hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s) {
-    if ((a.type != 12 && a.type != 14 && a.type != 8) || a.batch < 16 || a.batch > 64 || a.cols % 256)
+    if ((a.type != 12 && a.type != 13 && a.type != 14 && a.type != 8) || a.batch < 16 || a.batch > 64 || a.cols % 256)
         return hipErrorNotSupported;
-    if (a.type == 12 && ((reinterpret_cast<uintptr_t>(a.w) | a.pitch) & 15))
-        return hipErrorNotSupported;  // Q4_K rows are staged as whole aligned 16-byte chunks
+    if ((a.type == 12 || a.type == 13) && ((reinterpret_cast<uintptr_t>(a.w) | a.pitch) & 15))
+        return hipErrorNotSupported;  // K-quant rows are staged as whole aligned 16-byte chunks
     const int B = a.batch, Bp = (B + 31) / 32 * 32;
     const int nrows = a.row_end - a.row_start;
     const int nsb = a.cols / 256;
@@ -541,6 +565,8 @@ hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s
 #define JH_GEMM(F, NT) mfma_gemm<F, NT, NT == 1 ? kPrefetch : 1><<<grid, kThreads, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B)
     if (a.type == 12) {
         if (Bp == 32) JH_GEMM(FmtQ4K, 1); else JH_GEMM(FmtQ4K, 2);
+    } else if (a.type == 13) {
+        if (Bp == 32) JH_GEMM(FmtQ5K, 1); else JH_GEMM(FmtQ5K, 2);
     } else if (a.type == 14) {
         if (Bp == 32) JH_GEMM(FmtQ6K, 1); else JH_GEMM(FmtQ6K, 2);
     } else {

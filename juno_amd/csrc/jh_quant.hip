@@ -37,6 +37,31 @@ __global__ void dequant_q4k(const uint8_t *__restrict__ W, int64_t nsub, float *
     for (int i = 0; i < 32; i++) o[i] = __fsub_rn(__fmul_rn(scale, (float)((qs[i] >> shift) & 0x0F)), mn);
 }
 
+// dequantizeQ5K (LlamaTransformerHandler.java:1052-1093): the Q4_K layout plus a
+// 5th bit per element in qh (bit j of qh[l] for sub-block j).
+__global__ void dequant_q5k(const uint8_t *__restrict__ W, int64_t nsub, float *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 32-element sub-block
+    if (t >= nsub) return;
+    const int64_t blk = t >> 3;
+    const int j = (int)(t & 7), g = j >> 1;
+    const uint8_t *bp = W + blk * 176;
+    const float d = half_bits_to_float(bp[0] | (bp[1] << 8));
+    const float dmin = half_bits_to_float(bp[2] | (bp[3] << 8));
+    const uint32_t s0 = bp[4] | (bp[5] << 8) | (bp[6] << 16) | ((uint32_t)bp[7] << 24);
+    const uint32_t s1 = bp[8] | (bp[9] << 8) | (bp[10] << 16) | ((uint32_t)bp[11] << 24);
+    const uint32_t s2 = bp[12] | (bp[13] << 8) | (bp[14] << 16) | ((uint32_t)bp[15] << 24);
+    int ls, lm;
+    q4k_scale_min(s0, s1, s2, j, ls, lm);
+    const float scale = __fmul_rn(d, (float)ls), mn = __fmul_rn(dmin, (float)lm);
+    const uint8_t *qh = bp + 16, *qs = bp + 48 + g * 32;
+    const int shift = (j & 1) * 4;
+    float *o = out + t * 32;
+    for (int i = 0; i < 32; i++) {
+        const int q = ((qs[i] >> shift) & 0x0F) | (((qh[i] >> j) & 1) << 4);
+        o[i] = __fsub_rn(__fmul_rn(scale, (float)q), mn);
+    }
+}
+
 __global__ void dequant_q6k(const uint8_t *__restrict__ W, int64_t nsub, float *__restrict__ out) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 16-element sub-block
     if (t >= nsub) return;
@@ -74,7 +99,8 @@ hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float 
     const int64_t n = (int64_t)rows * cols;
     int64_t units;
     switch (type) {
-    case 12: units = n / 32; break;
+    case 12:
+    case 13: units = n / 32; break;
     case 14: units = n / 16; break;
     case 8: units = n / 32; break;
     case 0: units = n; break;
@@ -84,6 +110,7 @@ hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float 
     dim3 block(256), grid((unsigned)((units + 255) / 256));
     switch (type) {
     case 12: dequant_q4k<<<grid, block, 0, s>>>(w, units, out); break;
+    case 13: dequant_q5k<<<grid, block, 0, s>>>(w, units, out); break;
     case 14: dequant_q6k<<<grid, block, 0, s>>>(w, units, out); break;
     case 8: dequant_q8_0<<<grid, block, 0, s>>>(w, units, out); break;
     case 0: copy_f32<<<grid, block, 0, s>>>(reinterpret_cast<const float *>(w), units, out); break;
@@ -152,12 +179,17 @@ __global__ void quant_q8_0(const float *__restrict__ src, int64_t nblk, uint8_t 
     for (int i = 0; i < 32; i++) o[2 + i] = (uint8_t)(int8_t)clampi(java_round(__fmul_rn(v[i], invD)), -127, 127);
 }
 
-// quantizeQ4_K (LoraMerge.java:311-366); the nibbles use the fp32 d / dmin.
-__global__ void quant_q4k(const float *__restrict__ src, int64_t nblk, uint8_t *__restrict__ dst) {
+// quantizeQ4_K (LoraMerge.java:311-366) and quantizeQ5_K (:376-430): the same
+// scale / min search with q in [0, 15] (d = maxRange / 945) or [0, 31]
+// (d = maxRange / 1953, 5th bits in qh); the quants use the fp32 d / dmin.
+template <bool Q5>
+__global__ void quant_kq(const float *__restrict__ src, int64_t nblk, uint8_t *__restrict__ dst) {
+    constexpr int kBytes = Q5 ? 176 : 144, kQs = Q5 ? 48 : 16, kQmax = Q5 ? 31 : 15;
+    constexpr float kRange = Q5 ? 1953.f : 945.f;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= nblk) return;
     const float *v = src + t * 256;
-    uint8_t *o = dst + t * 144;
+    uint8_t *o = dst + t * kBytes;
     float mins[8], ranges[8];
     for (int s = 0; s < 8; s++) {
         float mn = 3.40282347e+38f, mx = -3.40282347e+38f;
@@ -179,7 +211,7 @@ __global__ void quant_q4k(const float *__restrict__ src, int64_t nblk, uint8_t *
         const float am = -mins[s];
         if (am > maxAbsMin) maxAbsMin = am;
     }
-    const float d = maxRange > 0.f ? __fdiv_rn(maxRange, 945.f) : 0.f;
+    const float d = maxRange > 0.f ? __fdiv_rn(maxRange, kRange) : 0.f;
     const float dmin = maxAbsMin > 0.f ? __fdiv_rn(maxAbsMin, 63.f) : 0.f;
     int ls[8], lm[8];
     for (int s = 0; s < 8; s++) {
@@ -193,16 +225,21 @@ __global__ void quant_q4k(const float *__restrict__ src, int64_t nblk, uint8_t *
         o[8 + j] = (uint8_t)((lm[j] & 0x3F) | ((lm[j + 4] & 0x30) << 2));
         o[12 + j] = (uint8_t)((ls[j + 4] & 0x0F) | ((lm[j + 4] & 0x0F) << 4));
     }
+    uint32_t qh[8] = {};  // 32 bytes of 5th bits, built in registers
     for (int g = 0; g < 4; g++) {
         const int s0 = 2 * g, s1 = s0 + 1;
         const float sc0 = __fmul_rn(d, (float)ls[s0]), mn0 = __fmul_rn(dmin, (float)lm[s0]);
         const float sc1 = __fmul_rn(d, (float)ls[s1]), mn1 = __fmul_rn(dmin, (float)lm[s1]);
         for (int i = 0; i < 32; i++) {
-            const int q0 = sc0 > 0.f ? clampi(java_round(__fdiv_rn(__fadd_rn(v[s0 * 32 + i], mn0), sc0)), 0, 15) : 0;
-            const int q1 = sc1 > 0.f ? clampi(java_round(__fdiv_rn(__fadd_rn(v[s1 * 32 + i], mn1), sc1)), 0, 15) : 0;
-            o[16 + g * 32 + i] = (uint8_t)(q0 | (q1 << 4));
+            const int q0 = sc0 > 0.f ? clampi(java_round(__fdiv_rn(__fadd_rn(v[s0 * 32 + i], mn0), sc0)), 0, kQmax) : 0;
+            const int q1 = sc1 > 0.f ? clampi(java_round(__fdiv_rn(__fadd_rn(v[s1 * 32 + i], mn1), sc1)), 0, kQmax) : 0;
+            o[kQs + g * 32 + i] = (uint8_t)((q0 & 0x0F) | ((q1 & 0x0F) << 4));
+            if (Q5)
+                qh[i >> 2] |= (uint32_t)((((q0 >> 4) & 1) << s0) | (((q1 >> 4) & 1) << s1)) << (8 * (i & 3));
         }
     }
+    if (Q5)
+        for (int i = 0; i < 32; i++) o[16 + i] = (uint8_t)(qh[i >> 2] >> (8 * (i & 3)));
 }
 
 // quantizeQ6_K (LoraMerge.java:437-469)
@@ -254,6 +291,7 @@ hipError_t launch_quantize(int type, const float *src, int64_t n, uint8_t *dst, 
     switch (type) {
     case 8: nblk = n / 32; break;
     case 12:
+    case 13:
     case 14: nblk = n / 256; break;
     case 0: return hipMemcpyAsync(dst, src, (size_t)n * 4, hipMemcpyDeviceToDevice, s);
     default: return hipErrorInvalidValue;
@@ -262,7 +300,8 @@ hipError_t launch_quantize(int type, const float *src, int64_t n, uint8_t *dst, 
     dim3 block(128), grid((unsigned)((nblk + 127) / 128));
     switch (type) {
     case 8: quant_q8_0<<<grid, block, 0, s>>>(src, nblk, dst); break;
-    case 12: quant_q4k<<<grid, block, 0, s>>>(src, nblk, dst); break;
+    case 12: quant_kq<false><<<grid, block, 0, s>>>(src, nblk, dst); break;
+    case 13: quant_kq<true><<<grid, block, 0, s>>>(src, nblk, dst); break;
     case 14: quant_q6k<<<grid, block, 0, s>>>(src, nblk, dst); break;
     }
     return hipGetLastError();

@@ -46,10 +46,10 @@ class UnsupportedOperationException(NotImplementedError):
     pass
 
 
-F32, Q8_0, Q4_K, Q6_K = 0, 8, 12, 14
-SUPPORTED_TYPES = (F32, Q8_0, Q4_K, Q6_K)
-_QK = {F32: 1, Q8_0: 32, Q4_K: 256, Q6_K: 256}
-_BLOCK_BYTES = {F32: 4, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
+SUPPORTED_TYPES = (F32, Q8_0, Q4_K, Q5_K, Q6_K)
+_QK = {F32: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+_BLOCK_BYTES = {F32: 4, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 
 
 def raw_byte_count(qtype: int, nelems: int) -> int:
@@ -67,6 +67,7 @@ class MatVecBackend(enum.Enum):
     ROCM_RESIDENT_FP16 = "rocm-resident-fp16"
     # new: packed weights resident on the device, fused dequant-GEMV
     ROCM_RESIDENT_Q4K = "rocm-resident-q4k"
+    ROCM_RESIDENT_Q5K = "rocm-resident-q5k"
     ROCM_RESIDENT_Q6K = "rocm-resident-q6k"
     ROCM_RESIDENT_Q8_0 = "rocm-resident-q8_0"
 
@@ -76,7 +77,7 @@ class MatVecBackend(enum.Enum):
 
     @staticmethod
     def for_type(qtype: int) -> "MatVecBackend":
-        return {F32: MatVecBackend.ROCM_RESIDENT, Q4_K: MatVecBackend.ROCM_RESIDENT_Q4K,
+        return {F32: MatVecBackend.ROCM_RESIDENT, Q4_K: MatVecBackend.ROCM_RESIDENT_Q4K, Q5_K: MatVecBackend.ROCM_RESIDENT_Q5K,
                 Q6_K: MatVecBackend.ROCM_RESIDENT_Q6K, Q8_0: MatVecBackend.ROCM_RESIDENT_Q8_0}[qtype]
 
 

@@ -64,7 +64,7 @@ def upload(be, qtype, raw, rows, cols):
 
 # ------------------------------------------------------------------ dequant
 
-@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K, O.F32])
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K, O.F32])
 @pytest.mark.parametrize("outliers", [False, True])
 def test_dequant_bit_exact(be, qtype, outliers):
     rows, cols = 96, 1024
@@ -126,7 +126,7 @@ def test_golden_q6k_block(be, golden):
 
 # ------------------------------------------------------------------ quantizer
 
-@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K])
 @pytest.mark.parametrize("outliers", [False, True])
 def test_device_quantizer_bit_exact(be, qtype, outliers):
     import torch
@@ -151,6 +151,9 @@ SHAPES = [
     (O.Q4_K, 256, 5632),     # nb = 22, not a multiple of 8
     (O.Q4_K, 1, 256),        # one row, one block
     (O.Q4_K, 37, 768),       # ragged rows, nb = 3
+    (O.Q5_K, 3072, 3072),    # Phi-3.5 Q4_K_M uses Q5_K (PhiQuantizedMatVecTest.java:242-248)
+    (O.Q5_K, 300, 5632),     # nb = 22
+    (O.Q5_K, 1, 256),
     (O.Q6_K, 2048, 5632),    # TinyLlama ffn_down (4620-byte rows)
     (O.Q6_K, 1000, 3072),    # Phi-3 sizes, odd row count
     (O.Q6_K, 3, 256),
@@ -210,8 +213,18 @@ def test_known_answers(be, golden):
             assert list(be.sgemv_quant(dev, x, a, b)) == g["expected_dot_ones"][a:b]
 
 
+def test_known_answer_q5k(be, golden):
+    g = golden["q5k_ones"]  # PhiQuantizedMatVecTest.java:255-290
+    blk = np.zeros(176, dtype=np.uint8)
+    blk[0:2] = [g["d_f16"] & 0xFF, g["d_f16"] >> 8]
+    blk[4] = g["sc0"]
+    blk[48:] = g["qs_fill"]
+    with upload(be, O.Q5_K, blk, 1, 256) as dev:
+        assert be.sgemv_quant(dev, np.ones(256, np.float32))[0] == g["expected_dot_ones"]
+
+
 def test_zero_inputs(be):
-    for qtype in (O.Q4_K, O.Q6_K, O.Q8_0):
+    for qtype in (O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0):
         rows, cols = 64, 512
         raw = O.quantize(qtype, weights(rows * cols, 3))
         with upload(be, qtype, raw, rows, cols) as dev:
@@ -232,7 +245,7 @@ def test_x_not_mutated(be):
 
 
 @pytest.mark.parametrize("B", [1, 2, 3, 5, 8, 11, 16, 20, 32, 48, 64])
-@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.Q8_0])
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0])
 def test_batched_vs_independent(be, qtype, B):
     rows, cols = 1024, 2048
     say("batched", qtype, B)
@@ -252,6 +265,7 @@ def test_batched_vs_independent(be, qtype, B):
 MFMA_SHAPES = [
     (O.Q4_K, 14336, 4096),   # 8B gate/up: one K split per 4 super-blocks
     (O.Q4_K, 1024, 4096),    # 8B k/v: K split 16 ways
+    (O.Q5_K, 3072, 3072),    # Phi-3.5 Q4_K_M's Q5_K projections
     (O.Q6_K, 4096, 14336),   # 8B ffn_down (Q4_K_M)
     (O.Q6_K, 1024, 4096),    # 8B attn_v (Q4_K_M)
     (O.Q8_0, 9216, 3072),    # Phi-3 fused QKV
@@ -276,7 +290,7 @@ def test_batched_mfma_8b_shapes(be, qtype, rows, cols):
                 assert rel_err(Y[j], ref, deq, X[j]).max() <= TOL, (rows, B, j)
 
 
-@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.Q8_0])
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0])
 def test_batched_mfma_odd_pitch_row_range(be, qtype):
     """Rows whose blocks start at 2 (mod 4) bytes (Q6_K / Q8_0 with 3 super-blocks
     per row), a row range that starts mid-tile, and a batch that is not a multiple of 32."""

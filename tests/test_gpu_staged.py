@@ -25,6 +25,7 @@ shapes = [
     (O.Q4_K, 5632, 2048), (O.Q4_K, 3001, 4096), (O.Q4_K, 1, 256), (O.Q4_K, 37, 768),
     (O.Q4_K, 700, 5632),            # 22 blocks: two column tiles
     (O.Q4_K, 300, 14336),           # 56 blocks: four column tiles
+    (O.Q5_K, 3072, 3072), (O.Q5_K, 700, 5632), (O.Q5_K, 300, 14336), (O.Q5_K, 5, 256),
     (O.Q6_K, 2048, 5632), (O.Q6_K, 999, 3072), (O.Q6_K, 3, 256), (O.Q6_K, 513, 14336),
     (O.Q8_0, 2304, 3072), (O.Q8_0, 129, 8192), (O.Q8_0, 5, 32), (O.Q8_0, 77, 2080),
 ]
@@ -52,7 +53,8 @@ for qtype, rows, cols in shapes:
             assert rel.max() <= 1e-3, (qtype, rows, cols, a, b, rel.max())
 # several matrices of one format sharing x in one staged launch (incl. column tiles)
 import torch
-for qtype, cols, rows_list in [(O.Q4_K, 4096, [333, 1000, 77]), (O.Q6_K, 14336, [129, 64]), (O.Q8_0, 3072, [500, 501, 7, 90])]:
+for qtype, cols, rows_list in [(O.Q4_K, 4096, [333, 1000, 77]), (O.Q5_K, 3072, [700, 300]), (O.Q6_K, 14336, [129, 64]),
+                               (O.Q8_0, 3072, [500, 501, 7, 90])]:
     rng = np.random.default_rng(cols + len(rows_list))
     x = rng.standard_normal(cols).astype(np.float32)
     dx = torch.from_numpy(x).cuda()
