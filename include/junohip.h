@@ -49,6 +49,8 @@ enum {
     JH_EUNSUPPORTED = 4, /* UnsupportedOperationException (ggml type) */
     JH_ECLOSED = 5,      /* IllegalStateException("... is closed") */
     JH_ENODEV = 6,       /* no usable gfx950 device */
+    JH_EFORMAT = 7,      /* IOException: not a GGUF / llamafile, bad header or metadata */
+    JH_EIO = 8,          /* IOException: open / read failed or file truncated */
 };
 
 enum {
@@ -190,8 +192,80 @@ int jh_rope_attention_dev(const float *q, const float *k, const float *v, int n_
  * 796-797. */
 int jh_silu_mul_dev(const float *gate, const float *up, int n, float *out, void *stream);
 
+/* The embedding row of token clamp(*d_token, 0, rows - 1), dequantized into
+ * d_out[cols]: getInitialActivation (LlamaTransformerHandler.java:651-660) over
+ * the packed token_embd matrix kept resident instead of a host float[] copy.
+ * The token is read on the device, so a captured step can be replayed. */
+int jh_embed_dev(const jh_qmat *m, const int *d_token, float *d_out, void *stream);
+
 /* *d_pos += delta, on the device (for replaying a captured decode step). */
 int jh_pos_increment_dev(int *d_pos, int delta, void *stream);
+
+/* ---------------------------------------------------------------- GGUF files
+ *
+ * GgufReader (GgufReader.java) behind plain handles.  A file that does not
+ * start with the GGUF magic is read as a llamafile: a ZIP whose *.gguf entry is
+ * stored uncompressed (findGgufOffsetInZip, :808-1025, with the forward-scan
+ * fallback :1027-1134 and ZIP64 offsets :1136-1154).  Metadata keeps the
+ * reference's Java typing (readMetadataValue, :1189-1246): 8- and 16-bit
+ * integers sign-extended to int, 32-bit to int, 64-bit to long. */
+typedef struct jh_gguf jh_gguf;
+
+enum {
+    JH_GGUF_UINT8 = 0, JH_GGUF_INT8 = 1, JH_GGUF_UINT16 = 2, JH_GGUF_INT16 = 3, JH_GGUF_UINT32 = 4,
+    JH_GGUF_INT32 = 5, JH_GGUF_FLOAT32 = 6, JH_GGUF_BOOL = 7, JH_GGUF_STRING = 8, JH_GGUF_ARRAY = 9,
+    JH_GGUF_UINT64 = 10, JH_GGUF_INT64 = 11, JH_GGUF_FLOAT64 = 12,
+};
+
+/* GgufReader.open (:102-183): header, metadata, tensor infos, data offset
+ * (aligned to 32 bytes from the start of the GGUF image).  JH_EFORMAT carries
+ * the reference's IOException messages. */
+int jh_gguf_open(const char *path, jh_gguf **out);
+
+/* GgufReader.close (:382-385).  NULL is accepted. */
+int jh_gguf_close(jh_gguf *g);
+
+/* GGUF version, header tensor / metadata counts, ggufFileOffset (:293),
+ * the data-section offset and metadataSectionEnd (:284).  Any out may be NULL. */
+int jh_gguf_info(const jh_gguf *g, int *version, int64_t *tensor_count, int64_t *kv_count, int64_t *gguf_offset,
+                 int64_t *data_offset, int64_t *metadata_end);
+
+/* meta(key) (:185): the value type (-1 when absent); for arrays the element
+ * type and count. */
+int jh_gguf_meta_type(const jh_gguf *g, const char *key, int *vtype, int *elem_type, int64_t *count);
+
+/* metaLong / metaInt / metaFloat (:194-207): present = the value is a Number;
+ * as_long = Number.longValue(), as_double = the exact value (a FLOAT32 value
+ * is exact in double, so floatValue() is (float)as_double). */
+int jh_gguf_meta_number(const jh_gguf *g, const char *key, int *present, int64_t *as_long, double *as_double);
+
+/* A BOOL entry (readMetadataValue :1220-1226): present = the key holds a bool. */
+int jh_gguf_meta_bool(const jh_gguf *g, const char *key, int *present, int *value);
+
+/* metaString (:189-192): *len = the UTF-8 byte length, or (size_t)-1 when the
+ * key is absent or not a string; up to cap-1 bytes and a NUL go to buf. */
+int jh_gguf_meta_string(const jh_gguf *g, const char *key, char *buf, size_t cap, size_t *len);
+
+/* Index of a tensor in file order (tensorOrder, :275), -1 when absent
+ * (hasTensor, :209).  A repeated name maps to its last entry. */
+int jh_gguf_tensor_index(const jh_gguf *g, const char *name, int64_t *index);
+
+/* tensorType / tensorDims / tensorNelems / tensorAbsoluteOffset (:225-270).
+ * dims receives ndims (<= 8) entries; *name stays valid until close. */
+int jh_gguf_tensor_info(const jh_gguf *g, int64_t index, const char **name, int *ggml_type, int *ndims,
+                        int64_t dims[8], int64_t *nelems, int64_t *abs_offset);
+
+/* tensorRaw (:329-345): the packed bytes, rawByteCount (:347-360) of them,
+ * into dst (cap bytes); *nbytes receives the size even when cap is short, and
+ * dst = NULL with cap = 0 only queries it. */
+int jh_gguf_tensor_read(const jh_gguf *g, int64_t index, void *dst, size_t cap, size_t *nbytes);
+
+/* tensorRaw + jh_qmat_upload in one pass: the tensor's bytes are streamed from
+ * the file through pinned staging into a new resident matrix with cols =
+ * dims[0] and rows = nelems / dims[0] (the ggml layout the reference's handlers
+ * use, LlamaTransformerHandler.java:296-358).  No host copy of the whole
+ * tensor is made. */
+int jh_gguf_upload(jh_ctx *ctx, const jh_gguf *g, int64_t index, jh_qmat **out);
 
 #ifdef __cplusplus
 }

@@ -5,7 +5,9 @@ of ``include/junohip.h``); this package is the host-side mirror of the
 reference's matvec interface (``juno_amd.matvec``).
 """
 from .matvec import (F32, Q4_K, Q5_K, Q6_K, Q8_0, DeviceQuantMatrix, GpuContext, HipMatVec,  # noqa: F401
-                     IllegalArgumentException, IllegalStateException, MatVecBackend, QuantizedTensor,
+                     IllegalArgumentException, IllegalStateException, IOException, MatVecBackend, QuantizedTensor,
                      UnsupportedOperationException, device_count, device_info, raw_byte_count)
+
+from .gguf import GgufArray, GgufReader  # noqa: F401,E402
 
 __version__ = "0.1.0"

@@ -12,7 +12,7 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libjunohip.so")
 
-JH_OK, JH_EINVAL, JH_ENOMEM, JH_EHIP, JH_EUNSUPPORTED, JH_ECLOSED, JH_ENODEV = range(7)
+JH_OK, JH_EINVAL, JH_ENOMEM, JH_EHIP, JH_EUNSUPPORTED, JH_ECLOSED, JH_ENODEV, JH_EFORMAT, JH_EIO = range(9)
 
 # Every symbol include/junohip.h declares, with (restype, argtypes).
 _P = ctypes.c_void_p
@@ -45,6 +45,18 @@ SIGNATURES = {
     "jh_rope_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _P]),
     "jh_silu_mul_dev": (_I, [_P, _P, _I, _P, _P]),
     "jh_pos_increment_dev": (_I, [_P, _I, _P]),
+    "jh_embed_dev": (_I, [_P, _P, _P, _P]),
+    "jh_gguf_open": (_I, [ctypes.c_char_p, _P]),
+    "jh_gguf_close": (_I, [_P]),
+    "jh_gguf_info": (_I, [_P, _P, _P, _P, _P, _P, _P]),
+    "jh_gguf_meta_type": (_I, [_P, ctypes.c_char_p, _P, _P, _P]),
+    "jh_gguf_meta_number": (_I, [_P, ctypes.c_char_p, _P, _P, _P]),
+    "jh_gguf_meta_bool": (_I, [_P, ctypes.c_char_p, _P, _P]),
+    "jh_gguf_meta_string": (_I, [_P, ctypes.c_char_p, _P, ctypes.c_size_t, _P]),
+    "jh_gguf_tensor_index": (_I, [_P, ctypes.c_char_p, _P]),
+    "jh_gguf_tensor_info": (_I, [_P, ctypes.c_int64, _P, _P, _P, _P, _P, _P]),
+    "jh_gguf_tensor_read": (_I, [_P, ctypes.c_int64, _P, ctypes.c_size_t, _P]),
+    "jh_gguf_upload": (_I, [_P, _P, ctypes.c_int64, _P]),
 }
 
 _lib = None

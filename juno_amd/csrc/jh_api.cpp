@@ -35,6 +35,10 @@ struct jh_qmat {
     uint8_t *d_raw;  // owned; nbytes + kTailPad bytes
 };
 
+// jh_gguf.cpp: with d_dst null only the tensor's geometry is returned.
+int jh_gguf_stream_to_device(const jh_gguf *g, int64_t index, uint8_t *d_dst, int64_t *nbytes, int *type,
+                             int64_t *rows, int64_t *cols);
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -271,6 +275,11 @@ int set_device(int dev) {
 extern "C" {
 
 const char *jh_last_error(void) { return g_last_error.c_str(); }
+
+int jh_internal_fail(int code, const char *msg) {
+    if (code == JH_OK) return ok();
+    return fail(code, "%s", msg);
+}
 
 const char *jh_version(void) { return "junohip 0.1 gfx950"; }
 
@@ -648,6 +657,45 @@ int jh_pos_increment_dev(int *d_pos, int delta, void *stream) {
     if (!d_pos) return fail(JH_EINVAL, "d_pos must not be null");
     hipError_t e = jh::launch_pos_increment(d_pos, delta, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail("pos_increment launch", e);
+    return ok();
+}
+
+int jh_embed_dev(const jh_qmat *m, const int *d_token, float *d_out, void *stream) {
+    if (!m || !d_token || !d_out) return fail(JH_EINVAL, "matrix, token and out must not be null");
+    if (m->rows <= 0) return fail(JH_EINVAL, "embedding matrix has no rows");
+    int rc = set_device(m->ctx->device);
+    if (rc) return rc;
+    hipError_t e = jh::launch_dequant_row(m->type, m->d_raw, m->rows, m->cols, m->pitch, d_token, d_out,
+                                          (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("embedding launch", e);
+    return ok();
+}
+
+int jh_gguf_upload(jh_ctx *ctx, const jh_gguf *g, int64_t index, jh_qmat **out) {
+    if (!ctx || !g || !out) return fail(JH_EINVAL, "ctx, gguf and out must not be null");
+    int64_t nbytes = 0, rows = 0, cols = 0;
+    int type = 0;
+    int rc = jh_gguf_stream_to_device(g, index, nullptr, &nbytes, &type, &rows, &cols);
+    if (rc) return rc;
+    if (rows > INT32_MAX || cols > INT32_MAX)
+        return fail(JH_EINVAL, "tensor %lld is too large for a matrix: rows=%lld cols=%lld", (long long)index,
+                    (long long)rows, (long long)cols);
+    jh_qmat *m;
+    rc = qmat_alloc(ctx, type, (int)rows, (int)cols, &m);
+    if (rc) return rc;
+    if ((int64_t)m->nbytes != nbytes) {
+        jh_qmat_free(m);
+        return fail(JH_EINVAL, "tensor %lld: %lld bytes on file != %zu for rows=%lld cols=%lld", (long long)index,
+                    (long long)nbytes, m->nbytes, (long long)rows, (long long)cols);
+    }
+    rc = jh_gguf_stream_to_device(g, index, m->d_raw, nullptr, nullptr, nullptr, nullptr);
+    if (rc) {
+        std::string err = g_last_error;
+        jh_qmat_free(m);
+        g_last_error = err;
+        return rc;
+    }
+    *out = m;
     return ok();
 }
 

@@ -65,6 +65,9 @@ hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s
 
 // out[rows][cols] fp32, bit-exact with the reference dequantizers.
 hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float *out, hipStream_t s);
+// Row clamp(*d_token, 0, rows - 1) of a packed matrix with row pitch `pitch`, dequantized into out[cols].
+hipError_t launch_dequant_row(int type, const uint8_t *w, int rows, int cols, size_t pitch, const int *d_token,
+                              float *out, hipStream_t s);
 
 // n fp32 values -> packed blocks with the LoraMerge quantizers.
 hipError_t launch_quantize(int type, const float *src, int64_t n, uint8_t *dst, hipStream_t s);

@@ -17,9 +17,9 @@ namespace jh {
 
 // ---------------------------------------------------------------- dequant
 
-__global__ void dequant_q4k(const uint8_t *__restrict__ W, int64_t nsub, float *__restrict__ out) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 32-element sub-block
-    if (t >= nsub) return;
+// Each dequant_* function expands one unit (a 32- or 16-element sub-block, a
+// Q8_0 block or one F32 element) t of the packed image W into out.
+__device__ __forceinline__ void dequant_q4k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
     const int64_t blk = t >> 3;
     const int j = (int)(t & 7), g = j >> 1;
     const uint8_t *bp = W + blk * 144;
@@ -39,9 +39,7 @@ __global__ void dequant_q4k(const uint8_t *__restrict__ W, int64_t nsub, float *
 
 // dequantizeQ5K (LlamaTransformerHandler.java:1052-1093): the Q4_K layout plus a
 // 5th bit per element in qh (bit j of qh[l] for sub-block j).
-__global__ void dequant_q5k(const uint8_t *__restrict__ W, int64_t nsub, float *__restrict__ out) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 32-element sub-block
-    if (t >= nsub) return;
+__device__ __forceinline__ void dequant_q5k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
     const int64_t blk = t >> 3;
     const int j = (int)(t & 7), g = j >> 1;
     const uint8_t *bp = W + blk * 176;
@@ -62,9 +60,7 @@ __global__ void dequant_q5k(const uint8_t *__restrict__ W, int64_t nsub, float *
     }
 }
 
-__global__ void dequant_q6k(const uint8_t *__restrict__ W, int64_t nsub, float *__restrict__ out) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 16-element sub-block
-    if (t >= nsub) return;
+__device__ __forceinline__ void dequant_q6k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
     const int64_t blk = t >> 4;
     const int s = (int)(t & 15), half = s >> 3, k = (s & 7) >> 1, is = s & 1;
     const uint8_t *bp = W + blk * 210;
@@ -81,39 +77,79 @@ __global__ void dequant_q6k(const uint8_t *__restrict__ W, int64_t nsub, float *
     }
 }
 
-__global__ void dequant_q8_0(const uint8_t *__restrict__ W, int64_t nblk, float *__restrict__ out) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= nblk) return;
+__device__ __forceinline__ void dequant_q8_0(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
     const uint8_t *bp = W + t * 34;
     const float d = half_bits_to_float(bp[0] | (bp[1] << 8));
     float *o = out + t * 32;
     for (int i = 0; i < 32; i++) o[i] = __fmul_rn(d, (float)(int8_t)bp[2 + i]);
 }
 
-__global__ void copy_f32(const float *__restrict__ W, int64_t n, float *__restrict__ out) {
+__device__ __forceinline__ void dequant_f32(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
+    out[t] = reinterpret_cast<const float *>(W)[t];
+}
+
+template <int T> __device__ __forceinline__ void dequant_unit(const uint8_t *W, int64_t t, float *out) {
+    if constexpr (T == 12) dequant_q4k(W, t, out);
+    else if constexpr (T == 13) dequant_q5k(W, t, out);
+    else if constexpr (T == 14) dequant_q6k(W, t, out);
+    else if constexpr (T == 8) dequant_q8_0(W, t, out);
+    else dequant_f32(W, t, out);
+}
+
+template <int T> __global__ void dequant_k(const uint8_t *__restrict__ W, int64_t units, float *__restrict__ out) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t < n) out[t] = W[t];
+    if (t < units) dequant_unit<T>(W, t, out);
+}
+
+// Embedding lookup (getInitialActivation, LlamaTransformerHandler.java:651-660):
+// row clamp(*d_token, 0, rows - 1) of the packed matrix, dequantized.  The
+// token is read on the device so that a captured step can be replayed.
+template <int T>
+__global__ void dequant_row_k(const uint8_t *__restrict__ W, const int *__restrict__ d_token, int rows, size_t pitch,
+                              int64_t units, float *__restrict__ out) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= units) return;
+    const int tok = min(max(*d_token, 0), rows - 1);
+    dequant_unit<T>(W + (size_t)tok * pitch, t, out);
+}
+
+int64_t dequant_units(int type, int64_t n) {
+    switch (type) {
+    case 12:
+    case 13:
+    case 8: return n / 32;
+    case 14: return n / 16;
+    case 0: return n;
+    default: return -1;
+    }
 }
 
 hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float *out, hipStream_t s) {
-    const int64_t n = (int64_t)rows * cols;
-    int64_t units;
-    switch (type) {
-    case 12:
-    case 13: units = n / 32; break;
-    case 14: units = n / 16; break;
-    case 8: units = n / 32; break;
-    case 0: units = n; break;
-    default: return hipErrorInvalidValue;
-    }
+    const int64_t units = dequant_units(type, (int64_t)rows * cols);
+    if (units < 0) return hipErrorInvalidValue;
     if (units == 0) return hipSuccess;
     dim3 block(256), grid((unsigned)((units + 255) / 256));
     switch (type) {
-    case 12: dequant_q4k<<<grid, block, 0, s>>>(w, units, out); break;
-    case 13: dequant_q5k<<<grid, block, 0, s>>>(w, units, out); break;
-    case 14: dequant_q6k<<<grid, block, 0, s>>>(w, units, out); break;
-    case 8: dequant_q8_0<<<grid, block, 0, s>>>(w, units, out); break;
-    case 0: copy_f32<<<grid, block, 0, s>>>(reinterpret_cast<const float *>(w), units, out); break;
+    case 12: dequant_k<12><<<grid, block, 0, s>>>(w, units, out); break;
+    case 13: dequant_k<13><<<grid, block, 0, s>>>(w, units, out); break;
+    case 14: dequant_k<14><<<grid, block, 0, s>>>(w, units, out); break;
+    case 8: dequant_k<8><<<grid, block, 0, s>>>(w, units, out); break;
+    case 0: dequant_k<0><<<grid, block, 0, s>>>(w, units, out); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_row(int type, const uint8_t *w, int rows, int cols, size_t pitch, const int *d_token,
+                              float *out, hipStream_t s) {
+    const int64_t units = dequant_units(type, cols);
+    if (units < 0 || rows <= 0) return hipErrorInvalidValue;
+    dim3 block(64), grid((unsigned)((units + 63) / 64));
+    switch (type) {
+    case 12: dequant_row_k<12><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
+    case 13: dequant_row_k<13><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
+    case 14: dequant_row_k<14><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
+    case 8: dequant_row_k<8><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
+    case 0: dequant_row_k<0><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
     }
     return hipGetLastError();
 }

@@ -27,7 +27,8 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _lib
-from .matvec import (Q4_K, Q6_K, DeviceQuantMatrix, GpuContext, IllegalArgumentException, _check)
+from .matvec import (Q4_K, Q6_K, DeviceQuantMatrix, GpuContext, IllegalArgumentException, IllegalStateException,
+                     UnsupportedOperationException, _check)
 
 _V = ctypes.c_void_p
 
@@ -35,6 +36,13 @@ _V = ctypes.c_void_p
 def _torch():
     import torch  # device memory and streams: plumbing around the HIP library
     return torch
+
+
+def _java_idiv(a: int, b: int) -> int:
+    """Java int division (truncates toward zero); int overflow of a * 11 is
+    not reproduced (hidden sizes are far below 2^31 / 11)."""
+    q = abs(a) // abs(b)
+    return q if (a >= 0) == (b >= 0) else -q
 
 
 @dataclass
@@ -48,6 +56,31 @@ class LlamaConfig:
     vocab_size: int
     rms_norm_eps: float = 1e-5
     rope_theta: float = 10000.0
+    architecture: str = "llama"
+
+    @classmethod
+    def from_gguf(cls, r) -> "LlamaConfig":
+        """LlamaConfig.from(GgufReader) (LlamaConfig.java:58-100): the architecture
+        prefix's keys first, then the llama.* keys, then the reference's defaults;
+        the vocabulary is the larger of the declared size and the length of
+        tokenizer.ggml.tokens (LlamaConfig.java:106-109)."""
+        arch = r.meta_string("general.architecture")
+        if arch is None:
+            arch = "llama"
+        p = arch + "."
+        hidden = r.meta_int(p + "embedding_length", r.meta_int("llama.embedding_length", 2048))
+        layers = r.meta_int(p + "block_count", r.meta_int("llama.block_count", 22))
+        heads = r.meta_int(p + "attention.head_count", r.meta_int("llama.attention.head_count", 32))
+        kv_heads = r.meta_int(p + "attention.head_count_kv", r.meta_int("llama.attention.head_count_kv", heads))
+        arch_vocab = r.meta_int(p + "vocab_size", r.meta_int("llama.vocab_size", 32000))
+        toks = r.meta("tokenizer.ggml.tokens")
+        tok_vocab = len(toks) if hasattr(toks, "elem_type") else 0
+        vocab = max(arch_vocab, tok_vocab)
+        ffn = r.meta_int(p + "feed_forward_length", r.meta_int("llama.feed_forward_length", _java_idiv(hidden * 11, 4)))
+        eps = r.meta_float(p + "attention.layer_norm_rms_epsilon",
+                           r.meta_float("llama.attention.layer_norm_rms_epsilon", 1e-5))
+        theta = r.meta_float(p + "rope.freq_base", r.meta_float("llama.rope.freq_base", 10000.0))
+        return cls(hidden, layers, heads, kv_heads, _java_idiv(hidden, heads), ffn, vocab, eps, theta, arch)
 
     @property
     def kv_dim(self) -> int:
@@ -88,12 +121,66 @@ class LlamaWeights:
     output_norm: object
     output: DeviceQuantMatrix
     keep: list = field(default_factory=list)
+    token_embd: DeviceQuantMatrix | None = None  # packed [vocab][hidden], for token input
 
     def close(self) -> None:
         for lw in self.layers:
             for m in lw.mats.values():
                 m.close()
         self.output.close()
+        if self.token_embd is not None and self.token_embd is not self.output:
+            self.token_embd.close()
+
+    # GGUF tensor names of a layer's projections (LlamaTransformerHandler.java:267-275)
+    GGUF_NAMES = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate",
+                  "up": "ffn_up", "down": "ffn_down"}
+
+    @classmethod
+    def from_gguf(cls, r, cfg: LlamaConfig | None = None, device: int = 0) -> "LlamaWeights":
+        """Every layer of a GGUF model, streamed from the file into HBM packed
+        (LlamaTransformerHandler.java:238-280, 459-470): blk.N.attn_norm /
+        ffn_norm (F32 / F16 / BF16, widened on the host), the seven projections,
+        output_norm, output.weight (token_embd.weight when the embeddings are
+        tied) and token_embd.weight for token input."""
+        torch = _torch()
+        cfg = cfg or LlamaConfig.from_gguf(r)
+        cfg.validate()
+        if cfg.num_layers > 0 and r.has_tensor("blk.0.attn_q.bias"):
+            raise UnsupportedOperationException(
+                "Q/K/V projection biases (LlamaTransformerHandler.java:258-280) are not on the device path")
+        be = GpuContext.shared(device).create_mat_vec()
+        dev = torch.device("cuda", device)
+        vec = lambda name: torch.from_numpy(np.ascontiguousarray(r.tensor(name), dtype=np.float32)).to(dev)
+        shapes = matrix_shapes(cfg)
+        made = []
+
+        def mat(name, rows, cols):
+            m = r.upload(name, be)
+            made.append(m)
+            if (m.rows, m.cols) != (rows, cols):
+                raise IllegalArgumentException(
+                    f"{name}: [{m.rows} x {m.cols}] on file, [{rows} x {cols}] expected from the config")
+            return m
+
+        try:
+            layers = []
+            for i in range(cfg.num_layers):
+                mats = {m: mat(f"blk.{i}.{cls.GGUF_NAMES[m]}.weight", *shapes[m]) for m in shapes}
+                layers.append(LlamaLayerWeights(vec(f"blk.{i}.attn_norm.weight"), vec(f"blk.{i}.ffn_norm.weight"),
+                                                mats))
+            embd = mat("token_embd.weight", cfg.vocab_size, cfg.hidden_dim) if r.has_tensor("token_embd.weight") \
+                else None
+            if r.has_tensor("output.weight"):
+                out = mat("output.weight", cfg.vocab_size, cfg.hidden_dim)
+            elif embd is not None:
+                out = embd  # tied embeddings
+            else:
+                raise IllegalArgumentException("Tensor not found: output.weight (and no token_embd.weight)")
+            return cls(cfg, layers, vec("output_norm.weight"), out, token_embd=embd)
+        except BaseException:
+            for m in made:
+                m.close()
+            raise
 
     @classmethod
     def random(cls, cfg: LlamaConfig, types: dict = Q4_K_M, seed: int = 0, device: int = 0,
@@ -170,6 +257,7 @@ class LlamaDecoder:
         self.hid = torch.zeros(c.intermediate_size, **f32)
         self.logits = torch.zeros(c.vocab_size, **f32)
         self.pos = torch.zeros(1, device=dev, dtype=torch.int32)
+        self.token = torch.zeros(1, device=dev, dtype=torch.int32)  # input token of a token step
 
     # ---------------------------------------------------------------- enqueue
     def _group(self, mats, xs, ys, s) -> None:
@@ -179,14 +267,19 @@ class LlamaDecoder:
         dy = (_V * n)(*[y.data_ptr() for y in ys])
         _check(self.L.jh_qmatvec_group_dev(n, handles, dx, dy, s))
 
-    def enqueue_step(self, stream=None, advance: bool = False) -> None:
+    def enqueue_step(self, stream=None, advance: bool = False, from_token: bool = False) -> None:
         """Enqueue one decode step on ``stream`` (a torch stream or None for the
         current one): x (the input activation) -> logits at position *pos.  With
+        from_token, x is first set to the embedding row of *token.  With
         advance, *pos += 1 on the device at the end (for graph replay)."""
         torch = _torch()
         c, L = self.cfg, self.L
         s = _V((stream or torch.cuda.current_stream()).cuda_stream)
         P = lambda t: _V(t.data_ptr())
+        if from_token:  # getInitialActivation (LlamaTransformerHandler.java:651-660)
+            if self.w.token_embd is None:
+                raise IllegalStateException("no token_embd.weight: this node takes activations")
+            _check(L.jh_embed_dev(self.w.token_embd.handle, P(self.token), P(self.x), s))
         eps, nh, nkv, hd, H = c.rms_norm_eps, c.num_heads, c.num_kv_heads, c.head_dim, c.hidden_dim
         for li, lw in enumerate(self.w.layers):
             if li == 0:  # rmsNorm(x) (LlamaTransformerHandler.java:748)
@@ -226,16 +319,29 @@ class LlamaDecoder:
         torch.cuda.synchronize()
         return self.logits.cpu().numpy()
 
-    def capture(self, stream):
+    def forward_token(self, token: int, pos: int) -> np.ndarray:
+        """logits for ``token`` at ``pos`` (the embedding row, clamped to the
+        vocabulary as getInitialActivation does, is the input activation)."""
+        torch = _torch()
+        if not 0 <= pos < self.max_seq:
+            raise IllegalArgumentException(f"pos {pos} outside [0, {self.max_seq})")
+        self.token.fill_(int(np.clip(token, -2**31, 2**31 - 1)))
+        self.pos.fill_(pos)
+        self.enqueue_step(from_token=True)
+        torch.cuda.synchronize()
+        return self.logits.cpu().numpy()
+
+    def capture(self, stream, from_token: bool = False):
         """A HIP graph of one step that also advances *pos; replay it after
-        writing the next activation into ``self.x``.  Capturing runs one eager
+        writing the next activation into ``self.x`` (or, with from_token, the next
+        token into ``self.token``).  Capturing runs one eager
         warm-up step first (it allocates the library's stream workspace outside
         the capture), which overwrites x, the logits and the KV row at *pos."""
         torch = _torch()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
-            self.enqueue_step(stream)  # warm-up: workspaces are allocated outside the capture
+            self.enqueue_step(stream, from_token=from_token)  # warm-up: workspaces are allocated outside the capture
             stream.synchronize()
             with torch.cuda.graph(g, stream=stream):
-                self.enqueue_step(stream, advance=True)
+                self.enqueue_step(stream, advance=True, from_token=from_token)
         return g

@@ -46,6 +46,10 @@ class UnsupportedOperationException(NotImplementedError):
     pass
 
 
+class IOException(OSError):
+    pass
+
+
 F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
 SUPPORTED_TYPES = (F32, Q8_0, Q4_K, Q5_K, Q6_K)
 _QK = {F32: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
@@ -98,6 +102,8 @@ def _check(rc: int) -> None:
         raise IllegalArgumentException(msg)
     if rc == _lib.JH_EUNSUPPORTED:
         raise UnsupportedOperationException(msg)
+    if rc in (_lib.JH_EFORMAT, _lib.JH_EIO):
+        raise IOException(msg)
     raise IllegalStateException(msg)
 
 
