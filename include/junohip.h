@@ -166,6 +166,11 @@ int jh_quantize_dev(int ggml_type, const float *d_src, int64_t n, void *d_dst, v
 int jh_rmsnorm_dev(const float *x, const float *res, const float *w, int n, float eps, float *x_out, float *out,
                    void *stream);
 
+/* jh_rmsnorm_dev over each row of [rows][n] (a batch of requests, one row
+ * each): forwardBatch's stacked activations (InferencePipeline.java:62-69). */
+int jh_rmsnorm_rows_dev(const float *x, const float *res, const float *w, int n, int rows, float eps, float *x_out,
+                        float *out, void *stream);
+
 /* Rotary embedding at position *d_pos (adjacent pairs) of q in place and of
  * k into k_cache[pos], and v copied into v_cache[pos]; caches hold max_seq
  * rows of n_kv_heads * head_dim floats.  rope: LlamaTransformerHandler.java:
@@ -188,6 +193,14 @@ int jh_rope_attention_dev(const float *q, const float *k, const float *v, int n_
                           const int *d_pos, int max_seq, float theta, float *k_cache, float *v_cache, float *out,
                           void *stream);
 
+/* jh_rope_attention_dev for `batch` requests in one launch pair: q [batch][n_heads*head_dim], k and v
+ * [batch][n_kv_heads*head_dim], out like q; request z is at position d_pos[z] and uses KV-cache slot
+ * d_slot[z] of caches laid out [n_slots][max_seq][n_kv_heads*head_dim] (one slot per request, the
+ * per-requestId caches of LlamaTransformerHandler.java:670-679).  forwardBatch, InferencePipeline.java:62-69. */
+int jh_rope_attention_batched_dev(const float *q, const float *k, const float *v, int batch, int n_heads,
+                                  int n_kv_heads, int head_dim, const int *d_pos, const int *d_slot, int n_slots,
+                                  int max_seq, float theta, float *k_cache, float *v_cache, float *out, void *stream);
+
 /* out = silu(gate) * up.  silu and ffn: LlamaTransformerHandler.java:1733-1735,
  * 796-797. */
 int jh_silu_mul_dev(const float *gate, const float *up, int n, float *out, void *stream);
@@ -197,6 +210,9 @@ int jh_silu_mul_dev(const float *gate, const float *up, int n, float *out, void 
  * the packed token_embd matrix kept resident instead of a host float[] copy.
  * The token is read on the device, so a captured step can be replayed. */
 int jh_embed_dev(const jh_qmat *m, const int *d_token, float *d_out, void *stream);
+
+/* jh_embed_dev for n tokens d_tokens[0..n) into d_out[n][cols] (a batch of requests). */
+int jh_embed_rows_dev(const jh_qmat *m, const int *d_tokens, int n, float *d_out, void *stream);
 
 /* *d_pos += delta, on the device (for replaying a captured decode step). */
 int jh_pos_increment_dev(int *d_pos, int delta, void *stream);

@@ -46,6 +46,10 @@ SIGNATURES = {
     "jh_silu_mul_dev": (_I, [_P, _P, _I, _P, _P]),
     "jh_pos_increment_dev": (_I, [_P, _I, _P]),
     "jh_embed_dev": (_I, [_P, _P, _P, _P]),
+    "jh_embed_rows_dev": (_I, [_P, _P, _I, _P, _P]),
+    "jh_rmsnorm_rows_dev": (_I, [_P, _P, _P, _I, _I, ctypes.c_float, _P, _P, _P]),
+    "jh_rope_attention_batched_dev": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, ctypes.c_float, _P, _P, _P,
+                                           _P]),
     "jh_gguf_open": (_I, [ctypes.c_char_p, _P]),
     "jh_gguf_close": (_I, [_P]),
     "jh_gguf_info": (_I, [_P, _P, _P, _P, _P, _P, _P]),

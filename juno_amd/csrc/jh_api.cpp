@@ -587,7 +587,19 @@ int jh_rmsnorm_dev(const float *x, const float *res, const float *w, int n, floa
     if (n < 1 || n > (1 << 20)) return fail(JH_EINVAL, "n=%d outside [1, 2^20]", n);
     if (!x || !w || !out) return fail(JH_EINVAL, "x, w and out must not be null");
     if (out == x || (x_out && out == x_out)) return fail(JH_EINVAL, "out must not alias x or x_out");
-    hipError_t e = jh::launch_rmsnorm(x, res, w, n, eps, x_out, out, (hipStream_t)stream);
+    hipError_t e = jh::launch_rmsnorm(x, res, w, n, 1, eps, x_out, out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("rmsnorm launch", e);
+    return ok();
+}
+
+int jh_rmsnorm_rows_dev(const float *x, const float *res, const float *w, int n, int rows, float eps, float *x_out,
+                        float *out, void *stream) {
+    if (n < 1 || n > (1 << 20)) return fail(JH_EINVAL, "n=%d outside [1, 2^20]", n);
+    if (rows < 0 || rows > 65535) return fail(JH_EINVAL, "rows=%d outside [0, 65535]", rows);
+    if (rows == 0) return ok();
+    if (!x || !w || !out) return fail(JH_EINVAL, "x, w and out must not be null");
+    if (out == x || (x_out && out == x_out)) return fail(JH_EINVAL, "out must not alias x or x_out");
+    hipError_t e = jh::launch_rmsnorm(x, res, w, n, rows, eps, x_out, out, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail("rmsnorm launch", e);
     return ok();
 }
@@ -622,11 +634,33 @@ static int attention_common(const float *q, const float *k_new, const float *v_n
     int dev = 0;
     JH_HIP("hipGetDevice", hipGetDevice(&dev));
     void *ws = nullptr;
-    if ((rc = stream_workspace(dev, (hipStream_t)stream, jh::attention_workspace_bytes(n_heads, head_dim, max_seq),
+    if ((rc = stream_workspace(dev, (hipStream_t)stream, jh::attention_workspace_bytes(n_heads, head_dim, max_seq, 1),
                                &ws)))
         return rc;
     hipError_t e = jh::launch_attention(q, k_new, v_new, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos,
                                         max_seq, theta, fused, out, ws, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("attention launch", e);
+    return ok();
+}
+
+int jh_rope_attention_batched_dev(const float *q, const float *k, const float *v, int batch, int n_heads,
+                                  int n_kv_heads, int head_dim, const int *d_pos, const int *d_slot, int n_slots,
+                                  int max_seq, float theta, float *k_cache, float *v_cache, float *out, void *stream) {
+    int rc;
+    if ((rc = check_heads(n_heads, n_kv_heads, head_dim, max_seq))) return rc;
+    if (batch < 0 || batch > 65535) return fail(JH_EINVAL, "batch=%d outside [0, 65535]", batch);
+    if (n_slots < 1) return fail(JH_EINVAL, "n_slots=%d must be >= 1", n_slots);
+    if (batch == 0) return ok();
+    if (!q || !k || !v || !d_pos || !d_slot || !k_cache || !v_cache || !out)
+        return fail(JH_EINVAL, "pointers must not be null");
+    int dev = 0;
+    JH_HIP("hipGetDevice", hipGetDevice(&dev));
+    void *ws = nullptr;
+    if ((rc = stream_workspace(dev, (hipStream_t)stream,
+                               jh::attention_workspace_bytes(n_heads, head_dim, max_seq, batch), &ws)))
+        return rc;
+    hipError_t e = jh::launch_attention(q, k, v, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos, max_seq, theta,
+                                        true, out, ws, (hipStream_t)stream, batch, d_slot, n_slots);
     if (e != hipSuccess) return hip_fail("attention launch", e);
     return ok();
 }
@@ -665,7 +699,20 @@ int jh_embed_dev(const jh_qmat *m, const int *d_token, float *d_out, void *strea
     if (m->rows <= 0) return fail(JH_EINVAL, "embedding matrix has no rows");
     int rc = set_device(m->ctx->device);
     if (rc) return rc;
-    hipError_t e = jh::launch_dequant_row(m->type, m->d_raw, m->rows, m->cols, m->pitch, d_token, d_out,
+    hipError_t e = jh::launch_dequant_row(m->type, m->d_raw, m->rows, m->cols, m->pitch, d_token, 1, d_out,
+                                          (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("embedding launch", e);
+    return ok();
+}
+
+int jh_embed_rows_dev(const jh_qmat *m, const int *d_tokens, int n, float *d_out, void *stream) {
+    if (n < 0 || n > 65535) return fail(JH_EINVAL, "n=%d outside [0, 65535]", n);
+    if (n == 0) return ok();
+    if (!m || !d_tokens || !d_out) return fail(JH_EINVAL, "matrix, tokens and out must not be null");
+    if (m->rows <= 0) return fail(JH_EINVAL, "embedding matrix has no rows");
+    int rc = set_device(m->ctx->device);
+    if (rc) return rc;
+    hipError_t e = jh::launch_dequant_row(m->type, m->d_raw, m->rows, m->cols, m->pitch, d_tokens, n, d_out,
                                           (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail("embedding launch", e);
     return ok();

@@ -24,11 +24,17 @@ namespace {
 // transformerLayer (:778, :783) is fused in front: v = x + res, x_out = v.
 constexpr int kNormThreads = 1024;
 
-// x_out may alias x (in-place residual); out must not alias x or x_out.
+// x_out may alias x (in-place residual); out must not alias x or x_out.  One
+// workgroup per row of [rows][n] (a batch of requests).
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_k(const float *x, const float *__restrict__ res,
                                                          const float *__restrict__ w, int n, float eps, float *x_out,
                                                          float *__restrict__ out) {
     __shared__ float part[kNormThreads / 64];
+    const size_t row = (size_t)blockIdx.x * n;
+    x += row;
+    if (res) res += row;
+    if (x_out) x_out += row;
+    out += row;
     float ss = 0.f;
     for (int i = threadIdx.x; i < n; i += kNormThreads) {
         const float v = res ? x[i] + res[i] : x[i];
@@ -114,8 +120,24 @@ __global__ __launch_bounds__(64) void attn_chunk_k(const float *__restrict__ q, 
                                                    const float *__restrict__ v_new, float *__restrict__ k_cache,
                                                    float *__restrict__ v_cache, int n_heads, int n_kv_heads,
                                                    int head_dim, const int *__restrict__ d_pos, int max_seq,
-                                                   float theta, float scale, float *__restrict__ part) {
+                                                   float theta, float scale, float *__restrict__ part,
+                                                   const int *__restrict__ d_slot, int n_slots) {
     extern __shared__ float lds[];
+    // request z of a batch: its q / k / v rows, position, cache slot and partials
+    const int z = blockIdx.z;
+    {
+        const int kvd = n_kv_heads * head_dim;
+        q += (size_t)z * n_heads * head_dim;
+        if (FUSED) {
+            k_new += (size_t)z * kvd;
+            v_new += (size_t)z * kvd;
+        }
+        d_pos += z;
+        const size_t cb = d_slot ? (size_t)min(max(d_slot[z], 0), n_slots - 1) * max_seq * kvd : 0;
+        k_cache += cb;
+        v_cache += cb;
+        part += (size_t)z * n_heads * gridDim.y * (head_dim + 2);
+    }
     const int tc = attn_tc(head_dim), kst = head_dim + 1;  // padded K rows: lane t in its own bank
     float *sk = lds;                  // [tc][head_dim + 1]
     float *sv = sk + tc * kst;        // [tc][head_dim]
@@ -192,7 +214,10 @@ __global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ 
                                                       float *__restrict__ out) {
     __shared__ float wc[1024];
     __shared__ float sL;
-    const int h = blockIdx.x, tc = attn_tc(head_dim);
+    const int h = blockIdx.x, tc = attn_tc(head_dim), z = blockIdx.y;  // head, request
+    d_pos += z;
+    part += (size_t)z * gridDim.x * nchmax * (head_dim + 2);
+    out += (size_t)z * gridDim.x * head_dim;
     const int T = min(*d_pos, max_seq - 1) + 1, nch = min((T + tc - 1) / tc, 1024);
     const float *ph = part + (size_t)h * nchmax * (head_dim + 2);
     float M = -INFINITY;
@@ -230,9 +255,9 @@ __global__ void pos_increment_k(int *d_pos, int delta) {
 
 }  // namespace
 
-hipError_t launch_rmsnorm(const float *x, const float *res, const float *w, int n, float eps, float *x_out,
+hipError_t launch_rmsnorm(const float *x, const float *res, const float *w, int n, int rows, float eps, float *x_out,
                           float *out, hipStream_t s) {
-    rmsnorm_k<<<1, kNormThreads, 0, s>>>(x, res, w, n, eps, x_out, out);
+    rmsnorm_k<<<rows, kNormThreads, 0, s>>>(x, res, w, n, eps, x_out, out);
     return hipGetLastError();
 }
 
@@ -245,19 +270,20 @@ hipError_t launch_rope_kv(float *q, const float *k, const float *v, int n_heads,
     return hipGetLastError();
 }
 
-size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq) {
+size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq, int batch) {
     const int nch = (max_seq + attn_tc(head_dim) - 1) / attn_tc(head_dim);
-    return (size_t)n_heads * nch * (head_dim + 2) * sizeof(float);
+    return (size_t)batch * n_heads * nch * (head_dim + 2) * sizeof(float);
 }
 
 hipError_t launch_attention(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
                             int n_heads, int n_kv_heads, int head_dim, const int *d_pos, int max_seq, float theta,
-                            bool fused, float *out, void *workspace, hipStream_t s) {
+                            bool fused, float *out, void *workspace, hipStream_t s, int batch, const int *d_slot,
+                            int n_slots) {
     const int tc = attn_tc(head_dim), nch = (max_seq + tc - 1) / tc;
     if (nch > 1024) return hipErrorNotSupported;  // combine weights live in a fixed LDS array
     const float scale = (float)(1.0 / sqrt((double)head_dim));
     float *part = static_cast<float *>(workspace);
-    const dim3 grid(n_heads, nch);
+    const dim3 grid(n_heads, nch, batch);
     const size_t lds = sizeof(float) * ((size_t)tc * (head_dim + 1) + (size_t)tc * head_dim + head_dim + tc);
     static const bool attr = [] {
         bool ok = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_chunk_k<true>),
@@ -268,13 +294,13 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
     (void)attr;
     if (fused)
         attn_chunk_k<true><<<grid, 64, lds, s>>>(q, k_new, v_new, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos,
-                                                max_seq, theta, scale, part);
+                                                max_seq, theta, scale, part, d_slot, n_slots);
     else
         attn_chunk_k<false><<<grid, 64, lds, s>>>(q, nullptr, nullptr, k_cache, v_cache, n_heads, n_kv_heads, head_dim,
-                                                 d_pos, max_seq, theta, scale, part);
+                                                 d_pos, max_seq, theta, scale, part, d_slot, n_slots);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attn_combine_k<<<n_heads, 256, 0, s>>>(part, head_dim, d_pos, max_seq, nch, out);
+    attn_combine_k<<<dim3(n_heads, batch), 256, 0, s>>>(part, head_dim, d_pos, max_seq, nch, out);
     return hipGetLastError();
 }
 

@@ -65,24 +65,28 @@ hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s
 
 // out[rows][cols] fp32, bit-exact with the reference dequantizers.
 hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float *out, hipStream_t s);
-// Row clamp(*d_token, 0, rows - 1) of a packed matrix with row pitch `pitch`, dequantized into out[cols].
-hipError_t launch_dequant_row(int type, const uint8_t *w, int rows, int cols, size_t pitch, const int *d_token,
-                              float *out, hipStream_t s);
+// Rows clamp(d_tokens[y], 0, rows - 1), y < n_out, of a packed matrix with row
+// pitch `pitch`, dequantized into out[y][cols].
+hipError_t launch_dequant_row(int type, const uint8_t *w, int rows, int cols, size_t pitch, const int *d_tokens,
+                              int n_out, float *out, hipStream_t s);
 
 // n fp32 values -> packed blocks with the LoraMerge quantizers.
 hipError_t launch_quantize(int type, const float *src, int64_t n, uint8_t *dst, hipStream_t s);
 
 // ---- the rest of a Llama decode step (jh_decode.hip); d_pos is a device int
-hipError_t launch_rmsnorm(const float *x, const float *res, const float *w, int n, float eps, float *x_out,
+hipError_t launch_rmsnorm(const float *x, const float *res, const float *w, int n, int rows, float eps, float *x_out,
                           float *out, hipStream_t s);
 hipError_t launch_rope_kv(float *q, const float *k, const float *v, int n_heads, int n_kv_heads, int head_dim,
                           const int *d_pos, int max_seq, float theta, float *k_cache, float *v_cache, hipStream_t s);
-size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq);
+size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq, int batch);
 // fused: q, k_new, v_new are this position's raw projections (rope + append
 // inside); otherwise q is rotated and the cache already holds the position
+// batch requests: q / k / v / out rows per request, d_pos[batch]; with d_slot the
+// caches are [n_slots][max_seq][kv_dim] and request z uses slot d_slot[z].
 hipError_t launch_attention(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
                             int n_heads, int n_kv_heads, int head_dim, const int *d_pos, int max_seq, float theta,
-                            bool fused, float *out, void *workspace, hipStream_t s);
+                            bool fused, float *out, void *workspace, hipStream_t s, int batch = 1,
+                            const int *d_slot = nullptr, int n_slots = 1);
 hipError_t launch_silu_mul(const float *gate, const float *up, int n, float *out, hipStream_t s);
 hipError_t launch_pos_increment(int *d_pos, int delta, hipStream_t s);
 

@@ -102,15 +102,16 @@ template <int T> __global__ void dequant_k(const uint8_t *__restrict__ W, int64_
 }
 
 // Embedding lookup (getInitialActivation, LlamaTransformerHandler.java:651-660):
-// row clamp(*d_token, 0, rows - 1) of the packed matrix, dequantized.  The
-// token is read on the device so that a captured step can be replayed.
+// for output row y = blockIdx.y, row clamp(d_tokens[y], 0, rows - 1) of the
+// packed matrix, dequantized into out[y].  Tokens are read on the device so
+// that a captured step can be replayed.
 template <int T>
-__global__ void dequant_row_k(const uint8_t *__restrict__ W, const int *__restrict__ d_token, int rows, size_t pitch,
-                              int64_t units, float *__restrict__ out) {
+__global__ void dequant_row_k(const uint8_t *__restrict__ W, const int *__restrict__ d_tokens, int rows, size_t pitch,
+                              int64_t units, int64_t row_elems, float *__restrict__ out) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= units) return;
-    const int tok = min(max(*d_token, 0), rows - 1);
-    dequant_unit<T>(W + (size_t)tok * pitch, t, out);
+    const int tok = min(max(d_tokens[blockIdx.y], 0), rows - 1);
+    dequant_unit<T>(W + (size_t)tok * pitch, t, out + (int64_t)blockIdx.y * row_elems);
 }
 
 int64_t dequant_units(int type, int64_t n) {
@@ -139,17 +140,17 @@ hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float 
     return hipGetLastError();
 }
 
-hipError_t launch_dequant_row(int type, const uint8_t *w, int rows, int cols, size_t pitch, const int *d_token,
-                              float *out, hipStream_t s) {
+hipError_t launch_dequant_row(int type, const uint8_t *w, int rows, int cols, size_t pitch, const int *d_tokens,
+                              int n_out, float *out, hipStream_t s) {
     const int64_t units = dequant_units(type, cols);
-    if (units < 0 || rows <= 0) return hipErrorInvalidValue;
-    dim3 block(64), grid((unsigned)((units + 63) / 64));
+    if (units < 0 || rows <= 0 || n_out < 1 || n_out > 65535) return hipErrorInvalidValue;
+    dim3 block(64), grid((unsigned)((units + 63) / 64), (unsigned)n_out);
     switch (type) {
-    case 12: dequant_row_k<12><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
-    case 13: dequant_row_k<13><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
-    case 14: dequant_row_k<14><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
-    case 8: dequant_row_k<8><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
-    case 0: dequant_row_k<0><<<grid, block, 0, s>>>(w, d_token, rows, pitch, units, out); break;
+    case 12: dequant_row_k<12><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
+    case 13: dequant_row_k<13><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
+    case 14: dequant_row_k<14><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
+    case 8: dequant_row_k<8><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
+    case 0: dequant_row_k<0><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
     }
     return hipGetLastError();
 }

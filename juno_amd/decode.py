@@ -184,9 +184,11 @@ class LlamaWeights:
 
     @classmethod
     def random(cls, cfg: LlamaConfig, types: dict = Q4_K_M, seed: int = 0, device: int = 0,
-               std: float = 0.02) -> "LlamaWeights":
+               std: float = 0.02, embeddings: bool = False) -> "LlamaWeights":
         """Random-init weights ~ N(0, std) drawn on the device and packed with the
-        device quantizer (bit-identical to LoraMerge's quantizers); norm weights 1 + N(0, 0.1^2)."""
+        device quantizer (bit-identical to LoraMerge's quantizers); norm weights
+        1 + N(0, 0.1^2).  With embeddings, a Q6_K token_embd [vocab][hidden] ~ N(0, 1)
+        for token input."""
         torch = _torch()
         cfg.validate()
         be = GpuContext.shared(device).create_mat_vec()
@@ -210,7 +212,14 @@ class LlamaWeights:
             mats = {n: qmat(types[n], *shapes[n]) for n in shapes}
             layers.append(LlamaLayerWeights(norm(), norm(), mats))
         out = qmat(types["output"], cfg.vocab_size, cfg.hidden_dim)
-        return cls(cfg, layers, norm(), out)
+        out_norm = norm()
+        embd = None
+        if embeddings:
+            w = torch.randn(cfg.vocab_size * cfg.hidden_dim, generator=g, device=dev, dtype=torch.float32)
+            embd = be.quantize_dev(Q6_K, w.data_ptr(), cfg.vocab_size, cfg.hidden_dim)
+            torch.cuda.synchronize()
+            del w
+        return cls(cfg, layers, out_norm, out, token_embd=embd)
 
     @classmethod
     def from_packed(cls, cfg: LlamaConfig, layers: list, output_norm, output_raw, output_type: int,
