@@ -320,7 +320,7 @@ def tinyllama_step(torch, stream, steps):
     from juno_amd import decode as D
     cfg = D.LlamaConfig(hidden_dim=2048, num_layers=22, num_heads=32, num_kv_heads=4, head_dim=64,
                         intermediate_size=5632, vocab_size=32000)
-    w = D.LlamaWeights.random(cfg, seed=7)
+    w = D.LlamaWeights.random(cfg, seed=7, embeddings=True)
     dec = D.LlamaDecoder(w, max_seq=512)
     g = torch.Generator(device="cuda")
     g.manual_seed(8)
@@ -353,8 +353,31 @@ def tinyllama_step(torch, stream, steps):
            "launches_per_step": cfg.num_layers * 9 + 2,
            "ops": "rmsnorm(+residual), grouped q/k/v, rope + KV append + GQA (2 kernels), o, grouped gate/up, "
                   "silu*up, down, final rmsnorm, output projection"}
+    del dec
+    out["batched"] = tinyllama_batch_step(torch, stream, steps, w, cfg, 32)
     w.close()
     return out
+
+
+def tinyllama_batch_step(torch, stream, steps, w, cfg, B):
+    """forwardBatch of B requests through the same TinyLlama-shaped model: one
+    decode step for all B (token embedding rows, batched GEMVs, batched rope +
+    KV append + attention over B cache slots), each request at position 511
+    over its own pre-filled KV cache; one captured graph per step."""
+    from juno_amd.pipeline import LlamaBatchPipeline
+    pipe = LlamaBatchPipeline(w, max_seq=512, max_batch=B)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(9)
+    pipe.k_cache.normal_(generator=g)
+    pipe.v_cache.normal_(generator=g)
+    rows = torch.tensor([[(97 * b) % cfg.vocab_size for b in range(B)], [511] * B, list(range(B))],
+                        dtype=torch.int32)
+    pipe.meta.copy_(rows)
+    ms, _ = time_graph(torch, lambda: pipe.enqueue(B, stream), stream, steps, 3)
+    del pipe
+    return {"config": f"tinyllama-1.1b-q4_k_m-forward-batch-b{B}-ctx512", "batch": B, "ms_per_step": round(ms, 4),
+            "tok_s": round(B * 1e3 / ms, 1),
+            "launches_per_step": cfg.num_layers * 12 + 3}
 
 
 def main():

@@ -115,44 +115,53 @@ __device__ __forceinline__ void rope_pair(float &x0, float &x1, int p, int head_
 // chunk's K and V)
 __host__ __device__ constexpr int attn_tc(int head_dim) { return head_dim <= 128 ? 64 : 32; }
 
+constexpr int kAttnWaves = 4;  // most waves per workgroup; they share the chunk's K and V
+
+// Split-sequence attention (gqa, LlamaTransformerHandler.java:1678-1731): one
+// workgroup per (KV head g, chunk c of tc positions, request z) stages the
+// chunk's K and V rows of head g in LDS once; its waves then take the query
+// heads h = g*R .. g*R+R-1 that share them (GQA), each writing the chunk's
+// (max score, sum of exp, sum of exp * v) for the combine kernel.  With FUSED,
+// rope (:1657-1671) is applied to q and to the new k, and the new k and v row
+// is appended to the cache at pos (transformerLayer :765-770) by the chunk that
+// holds pos, once per KV head.
 template <bool FUSED>
-__global__ __launch_bounds__(64) void attn_chunk_k(const float *__restrict__ q, const float *__restrict__ k_new,
-                                                   const float *__restrict__ v_new, float *__restrict__ k_cache,
-                                                   float *__restrict__ v_cache, int n_heads, int n_kv_heads,
-                                                   int head_dim, const int *__restrict__ d_pos, int max_seq,
-                                                   float theta, float scale, float *__restrict__ part,
-                                                   const int *__restrict__ d_slot, int n_slots) {
+__global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_k(
+    const float *__restrict__ q, const float *__restrict__ k_new, const float *__restrict__ v_new,
+    float *__restrict__ k_cache, float *__restrict__ v_cache, int n_heads, int n_kv_heads, int head_dim,
+    const int *__restrict__ d_pos, int max_seq, float theta, float scale, float *__restrict__ part,
+    const int *__restrict__ d_slot, int n_slots) {
     extern __shared__ float lds[];
+    const int tc = attn_tc(head_dim), kst = head_dim + 1;  // padded K rows: lane t in its own bank
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    float *sk = lds;                          // [tc][head_dim + 1]
+    float *sv = sk + tc * kst;                // [tc][head_dim]
+    float *sq = sv + tc * head_dim + wave * (head_dim + tc);  // this wave's [head_dim] q, then [tc] weights
+    float *sp = sq + head_dim;
     // request z of a batch: its q / k / v rows, position, cache slot and partials
-    const int z = blockIdx.z;
+    const int z = blockIdx.z, kv_dim = n_kv_heads * head_dim;
+    q += (size_t)z * n_heads * head_dim;
+    if (FUSED) {
+        k_new += (size_t)z * kv_dim;
+        v_new += (size_t)z * kv_dim;
+    }
     {
-        const int kvd = n_kv_heads * head_dim;
-        q += (size_t)z * n_heads * head_dim;
-        if (FUSED) {
-            k_new += (size_t)z * kvd;
-            v_new += (size_t)z * kvd;
-        }
-        d_pos += z;
-        const size_t cb = d_slot ? (size_t)min(max(d_slot[z], 0), n_slots - 1) * max_seq * kvd : 0;
+        const size_t cb = d_slot ? (size_t)min(max(d_slot[z], 0), n_slots - 1) * max_seq * kv_dim : 0;
         k_cache += cb;
         v_cache += cb;
-        part += (size_t)z * n_heads * gridDim.y * (head_dim + 2);
     }
-    const int tc = attn_tc(head_dim), kst = head_dim + 1;  // padded K rows: lane t in its own bank
-    float *sk = lds;                  // [tc][head_dim + 1]
-    float *sv = sk + tc * kst;        // [tc][head_dim]
-    float *sq = sv + tc * head_dim;   // [head_dim]
-    float *sp = sq + head_dim;        // [tc]
-    const int pos = min(*d_pos, max_seq - 1), T = pos + 1;
-    const int h = blockIdx.x, c = blockIdx.y, t0 = c * tc, lane = threadIdx.x;
-    if (t0 >= T) return;  // uniform across the wavefront
-    const int R = n_heads / n_kv_heads, g = h / R, kv_dim = n_kv_heads * head_dim;
+    part += (size_t)z * n_heads * gridDim.y * (head_dim + 2);
+    const int pos = min(d_pos[z], max_seq - 1), T = pos + 1;
+    const int g = blockIdx.x, c = blockIdx.y, t0 = c * tc;
+    if (t0 >= T) return;  // uniform across the workgroup
+    const int R = n_heads / n_kv_heads;
     const int nt = min(tc, T - t0);
     const bool has_pos = FUSED && pos < t0 + tc;  // this chunk holds the new position
-    // the chunk's K and V rows (cache positions; the new one is overwritten below)
+    // the chunk's K and V rows of head g (cache positions; the new one is written below)
     const int q4 = head_dim / 4, n4 = nt * q4;
-    for (int i = lane; i < n4; i += 64) {
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
         const int t = i / q4, d = 4 * (i % q4);
+        if (has_pos && t0 + t == pos) continue;
         const size_t o = (size_t)(t0 + t) * kv_dim + g * head_dim + d;
         const float4 kk = *reinterpret_cast<const float4 *>(k_cache + o);
         const float4 vv = *reinterpret_cast<const float4 *>(v_cache + o);
@@ -160,52 +169,64 @@ __global__ __launch_bounds__(64) void attn_chunk_k(const float *__restrict__ q, 
         kd[0] = kk.x; kd[1] = kk.y; kd[2] = kk.z; kd[3] = kk.w;
         *reinterpret_cast<float4 *>(sv + t * head_dim + d) = vv;
     }
-    __syncthreads();
-    for (int p = lane; p < head_dim / 2; p += 64) {
-        float a = q[h * head_dim + 2 * p], b = q[h * head_dim + 2 * p + 1];
-        if (FUSED) rope_pair(a, b, p, head_dim, pos, theta);
-        sq[2 * p] = a;
-        sq[2 * p + 1] = b;
-        if (has_pos) {
+    if (has_pos) {
+        const int tp = pos - t0;
+        for (int p = threadIdx.x; p < head_dim / 2; p += blockDim.x) {
             float ka = k_new[g * head_dim + 2 * p], kb = k_new[g * head_dim + 2 * p + 1];
             rope_pair(ka, kb, p, head_dim, pos, theta);
-            const int tp = pos - t0;
             sk[tp * kst + 2 * p] = ka;
             sk[tp * kst + 2 * p + 1] = kb;
             const size_t o = (size_t)pos * kv_dim + g * head_dim + 2 * p;
             k_cache[o] = ka;
             k_cache[o + 1] = kb;
         }
-    }
-    if (has_pos)
-        for (int d = lane; d < head_dim; d += 64) {
+        for (int d = threadIdx.x; d < head_dim; d += blockDim.x) {
             const float v = v_new[g * head_dim + d];
-            sv[(pos - t0) * head_dim + d] = v;
+            sv[tp * head_dim + d] = v;
             v_cache[(size_t)pos * kv_dim + g * head_dim + d] = v;
         }
-    __syncthreads();
-    float s = -INFINITY;
-    if (lane < nt) {
-        float dot = 0.f;
-        for (int d = 0; d < head_dim; d++) dot += sq[d] * sk[lane * kst + d];
-        s = dot * scale;
     }
-    float m = s;
+    __syncthreads();
+    for (int r = wave; r < R; r += nw) {  // wave-uniform
+        const int h = g * R + r;
+        for (int p = lane; p < head_dim / 2; p += 64) {
+            float a = q[h * head_dim + 2 * p], b = q[h * head_dim + 2 * p + 1];
+            if (FUSED) rope_pair(a, b, p, head_dim, pos, theta);
+            sq[2 * p] = a;
+            sq[2 * p + 1] = b;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float s = -INFINITY;
+        if (lane < nt) {
+            float dot = 0.f;
+            for (int d = 0; d < head_dim; d++) dot += sq[d] * sk[lane * kst + d];
+            s = dot * scale;
+        }
+        float m = s;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    const float e = lane < nt ? (float)exp((double)(s - m)) : 0.f;
-    const float l = wave_sum(e);
-    if (lane < tc) sp[lane] = e;
-    __syncthreads();
-    float *ph = part + ((size_t)h * gridDim.y + c) * (head_dim + 2);
-    for (int d = lane; d < head_dim; d += 64) {
-        float o = 0.f;
-        for (int t = 0; t < nt; t++) o += sp[t] * sv[t * head_dim + d];
-        ph[2 + d] = o;
-    }
-    if (lane == 0) {
-        ph[0] = m;
-        ph[1] = l;
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float e = lane < nt ? (float)exp((double)(s - m)) : 0.f;
+        const float l = wave_sum(e);
+        if (lane < tc) sp[lane] = e;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float *ph = part + ((size_t)h * gridDim.y + c) * (head_dim + 2);
+        for (int d = lane; d < head_dim; d += 64) {
+            float o = 0.f;
+            for (int t = 0; t < nt; t++) o += sp[t] * sv[t * head_dim + d];
+            ph[2 + d] = o;
+        }
+        if (lane == 0) {
+            ph[0] = m;
+            ph[1] = l;
+        }
+        // sq / sp are rewritten by this wave's next head
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
@@ -283,8 +304,10 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
     if (nch > 1024) return hipErrorNotSupported;  // combine weights live in a fixed LDS array
     const float scale = (float)(1.0 / sqrt((double)head_dim));
     float *part = static_cast<float *>(workspace);
-    const dim3 grid(n_heads, nch, batch);
-    const size_t lds = sizeof(float) * ((size_t)tc * (head_dim + 1) + (size_t)tc * head_dim + head_dim + tc);
+    const dim3 grid(n_kv_heads, nch, batch);
+    const int nw = min(n_heads / n_kv_heads, kAttnWaves);  // one wave per query head of a group, up to 4
+    const size_t lds = sizeof(float) * ((size_t)tc * (head_dim + 1) + (size_t)tc * head_dim +
+                                        (size_t)nw * (head_dim + tc));
     static const bool attr = [] {
         bool ok = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_chunk_k<true>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
@@ -293,10 +316,10 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
     }();
     (void)attr;
     if (fused)
-        attn_chunk_k<true><<<grid, 64, lds, s>>>(q, k_new, v_new, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos,
+        attn_chunk_k<true><<<grid, 64 * nw, lds, s>>>(q, k_new, v_new, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos,
                                                 max_seq, theta, scale, part, d_slot, n_slots);
     else
-        attn_chunk_k<false><<<grid, 64, lds, s>>>(q, nullptr, nullptr, k_cache, v_cache, n_heads, n_kv_heads, head_dim,
+        attn_chunk_k<false><<<grid, 64 * nw, lds, s>>>(q, nullptr, nullptr, k_cache, v_cache, n_heads, n_kv_heads, head_dim,
                                                  d_pos, max_seq, theta, scale, part, d_slot, n_slots);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
