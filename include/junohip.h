@@ -56,6 +56,8 @@ enum {
 enum {
     JH_TYPE_F32 = 0,
     JH_TYPE_Q8_0 = 8,
+    JH_TYPE_Q2_K = 10,
+    JH_TYPE_Q3_K = 11,
     JH_TYPE_Q4_K = 12,
     JH_TYPE_Q5_K = 13,
     JH_TYPE_Q6_K = 14,

@@ -96,6 +96,8 @@ bool type_geometry(int type, int *qk, int *bb) {
     switch (type) {
     case JH_TYPE_F32: *qk = 1; *bb = 4; return true;
     case JH_TYPE_Q8_0: *qk = 32; *bb = 34; return true;
+    case JH_TYPE_Q2_K: *qk = 256; *bb = 84; return true;
+    case JH_TYPE_Q3_K: *qk = 256; *bb = 110; return true;
     case JH_TYPE_Q4_K: *qk = 256; *bb = 144; return true;
     case JH_TYPE_Q5_K: *qk = 256; *bb = 176; return true;
     case JH_TYPE_Q6_K: *qk = 256; *bb = 210; return true;

@@ -4,7 +4,7 @@
 // (B = 1 is the decode GEMV).  The weights are streamed from HBM exactly once
 // in their packed layout; dequantization happens in registers.
 //
-// Work split (all three quantized kernels): a workgroup is 4 wavefronts, a
+// Work split (all quantized kernels): a workgroup is 4 wavefronts, a
 // wavefront owns R consecutive rows, and its 64 lanes sweep the row's blocks
 // as 8 blocks x 8 lanes per step.  All R rows share each lane's x values, so
 // x is read R times less than the weights would require.  Per-lane partial
@@ -216,6 +216,188 @@ __device__ __forceinline__ void gemv_q6k_body(int wg, const uint8_t *__restrict_
         }
 }
 
+// ---------------------------------------------------------------- Q2_K
+// matVecQ2Kraw (LlamaTransformerHandler.java:1303-1346), block [sc 16][qs 64][d][dmin].
+// Lane (kb, ch): block b = step*8 + kb; half h = ch/4, r = (ch/2)&1, l0 = 8*(ch&1).
+// The 8 qs bytes [32h + 16r + l0, +8) at shift 2j (j = 0..3) are the elements
+// h*128 + 16(2j + r) + l, l in [l0, l0+8), with scale byte sc[8h + 2j + r]
+// (low nibble scale, high nibble min): w = (d*scale)*q - dmin*min.  Folded per
+// run as d*scale*sum(q*x) - dmin*min*sum(x).
+template <int R, int B>
+__device__ __forceinline__ void gemv_q2k_body(int wg, const uint8_t *__restrict__ W, size_t pitch, int nb,
+                                                int nrows, const float *__restrict__ X, int ldx,
+                                                float *__restrict__ Y, int ldy) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r0 = (wg * 4 + wave) * R;
+    if (r0 >= nrows) return;
+    const int kb = lane >> 3, ch = lane & 7, h = ch >> 2, r = (ch >> 1) & 1, l0 = (ch & 1) * 8;
+
+    float acc[R][B];
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) acc[i][j] = 0.f;
+
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) rowp[i] = W + (size_t)min(r0 + i, nrows - 1) * pitch;
+
+    for (int b = kb; b < nb; b += 8) {
+        uint2 q[R], sc[R];
+        uint32_t dm[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const uint8_t *bp = rowp[i] + (size_t)b * 84;  // 4-byte aligned: 84 = 4 * 21
+            q[i] = load8_a2(bp + 16 + 32 * h + 16 * r + l0);
+            sc[i] = load8_a2(bp + 8 * h);
+            dm[i] = *reinterpret_cast<const uint32_t *>(bp + 80);
+        }
+        float xv[B][4][8], sx[B][4];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const float *xp = X + (size_t)j * ldx + b * 256 + h * 128 + 16 * r + l0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float4 a = load_f4(xp + 32 * k), c = load_f4(xp + 32 * k + 4);
+                xv[j][k][0] = a.x; xv[j][k][1] = a.y; xv[j][k][2] = a.z; xv[j][k][3] = a.w;
+                xv[j][k][4] = c.x; xv[j][k][5] = c.y; xv[j][k][6] = c.z; xv[j][k][7] = c.w;
+                float s = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) s += xv[j][k][e];
+                sx[j][k] = s;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const float d = half_bits_to_float(dm[i]), dmin = half_bits_to_float(dm[i] >> 16);
+            float dsc[4], dmn[4];
+            uint32_t u[4][2];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int idx = 2 * k + r;  // scale byte within the half
+                const uint32_t sb = byte_of(idx < 4 ? sc[i].x : sc[i].y, idx & 3);
+                dsc[k] = d * (float)(sb & 15u);
+                dmn[k] = dmin * (float)(sb >> 4);
+                u[k][0] = (q[i].x >> (2 * k)) & 0x03030303u;
+                u[k][1] = (q[i].y >> (2 * k)) & 0x03030303u;
+            }
+#pragma unroll
+            for (int j = 0; j < B; j++) {
+                float a = acc[i][j];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    float dot = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        dot = fmaf((float)byte_of(u[k][e >> 2], e & 3), xv[j][k][e], dot);
+                    a = fmaf(dsc[k], dot, a);
+                    a = fmaf(-dmn[k], sx[j][k], a);
+                }
+                acc[i][j] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            float s = wave_sum(acc[i][j]);
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+        }
+}
+
+// ---------------------------------------------------------------- Q3_K
+// matVecQ3Kraw (LlamaTransformerHandler.java:1358-1425), block [hmask 32][qs 64][scales 12][d].
+// Lane (kb, ch): block b = step*8 + kb; half h = ch/4, r = (ch/2)&1, l0 = 8*(ch&1).
+// Elements h*128 + 32j + 16r + l (j = 0..3, l in [l0, l0+8)) take the 2 bits at
+// shift 2j of qs[32h + 16r + l], bit 4h + j of hmask[16r + l] and the signed
+// scale sc[8h + 2j + r]: w = (d*sc) * (q - 4), folded as d*sc*(sum(q*x) - 4*sum(x)).
+// Blocks are 2-byte aligned (110 bytes).
+template <int R, int B>
+__device__ __forceinline__ void gemv_q3k_body(int wg, const uint8_t *__restrict__ W, size_t pitch, int nb,
+                                                int nrows, const float *__restrict__ X, int ldx,
+                                                float *__restrict__ Y, int ldy) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r0 = (wg * 4 + wave) * R;
+    if (r0 >= nrows) return;
+    const int kb = lane >> 3, ch = lane & 7, h = ch >> 2, r = (ch >> 1) & 1, l0 = (ch & 1) * 8;
+
+    float acc[R][B];
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) acc[i][j] = 0.f;
+
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) rowp[i] = W + (size_t)min(r0 + i, nrows - 1) * pitch;
+
+    for (int b = kb; b < nb; b += 8) {
+        uint2 q[R], hm[R], a01[R], a2d[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const uint8_t *bp = rowp[i] + (size_t)b * 110;
+            q[i] = load8_a2(bp + 32 + 32 * h + 16 * r + l0);
+            hm[i] = load8_a2(bp + 16 * r + l0);
+            a01[i] = load8_a2(bp + 96);   // scale words aux0, aux1
+            a2d[i] = load8_a2(bp + 104);  // aux2, then d in the low half of .y
+        }
+        float xv[B][4][8], sx[B][4];
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            const float *xp = X + (size_t)j * ldx + b * 256 + h * 128 + 16 * r + l0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float4 a = load_f4(xp + 32 * k), c = load_f4(xp + 32 * k + 4);
+                xv[j][k][0] = a.x; xv[j][k][1] = a.y; xv[j][k][2] = a.z; xv[j][k][3] = a.w;
+                xv[j][k][4] = c.x; xv[j][k][5] = c.y; xv[j][k][6] = c.z; xv[j][k][7] = c.w;
+                float s = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) s += xv[j][k][e];
+                sx[j][k] = s;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const float d = half_bits_to_float(a2d[i].y);
+            // the scale words of this half (dequantizeQ3K's utmp[2h], utmp[2h+1], :969-985)
+            const uint32_t aux2 = a2d[i].x;
+            const uint32_t ua = ((a01[i].x >> (4 * h)) & 0x0f0f0f0fu) | (((aux2 >> (4 * h)) & 0x03030303u) << 4);
+            const uint32_t ub = ((a01[i].y >> (4 * h)) & 0x0f0f0f0fu) | (((aux2 >> (4 * h + 2)) & 0x03030303u) << 4);
+            float dsc[4];
+            uint32_t u[4][2];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int s6 = (int)byte_of(k < 2 ? ua : ub, 2 * (k & 1) + r) - 32;
+                dsc[k] = d * (float)s6;
+                const int hb = 4 * h + k;
+                u[k][0] = ((q[i].x >> (2 * k)) & 0x03030303u) | (((hm[i].x >> hb) & 0x01010101u) << 2);
+                u[k][1] = ((q[i].y >> (2 * k)) & 0x03030303u) | (((hm[i].y >> hb) & 0x01010101u) << 2);
+            }
+#pragma unroll
+            for (int j = 0; j < B; j++) {
+                float a = acc[i][j];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    float dot = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        dot = fmaf((float)byte_of(u[k][e >> 2], e & 3), xv[j][k][e], dot);
+                    a = fmaf(dsc[k], fmaf(-4.f, sx[j][k], dot), a);
+                }
+                acc[i][j] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int j = 0; j < B; j++) {
+            float s = wave_sum(acc[i][j]);
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+        }
+}
+
 // ---------------------------------------------------------------- Q8_0
 // One lane per 34-byte block (32 weights); a wavefront step covers 64 blocks.
 // The block start is 2-byte aligned: ten aligned dwords cover it.
@@ -303,6 +485,16 @@ __global__ __launch_bounds__(256) void gemv_q5k(const uint8_t *__restrict__ W, s
     gemv_q4k_body<R, B, true>(blockIdx.x, W, pitch, nb, nrows, X, ldx, Y, ldy);
 }
 template <int R, int B>
+__global__ __launch_bounds__(256) void gemv_q2k(const uint8_t *__restrict__ W, size_t pitch, int nb, int nrows,
+                                                const float *__restrict__ X, int ldx, float *__restrict__ Y, int ldy) {
+    gemv_q2k_body<R, B>(blockIdx.x, W, pitch, nb, nrows, X, ldx, Y, ldy);
+}
+template <int R, int B>
+__global__ __launch_bounds__(256) void gemv_q3k(const uint8_t *__restrict__ W, size_t pitch, int nb, int nrows,
+                                                const float *__restrict__ X, int ldx, float *__restrict__ Y, int ldy) {
+    gemv_q3k_body<R, B>(blockIdx.x, W, pitch, nb, nrows, X, ldx, Y, ldy);
+}
+template <int R, int B>
 __global__ __launch_bounds__(256) void gemv_q6k(const uint8_t *__restrict__ W, size_t pitch, int nb, int nrows,
                                                 const float *__restrict__ X, int ldx, float *__restrict__ Y, int ldy) {
     gemv_q6k_body<R, B>(blockIdx.x, W, pitch, nb, nrows, X, ldx, Y, ldy);
@@ -331,6 +523,8 @@ __global__ __launch_bounds__(256) void gemv_group(GroupArgs g) {
         case 12: gemv_q4k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         case 13: gemv_q4k_body<2, 1, true>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         case 14: gemv_q6k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
+        case 10: gemv_q2k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
+        case 11: gemv_q3k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         default: gemv_q8_0_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         }
     } else {
@@ -338,6 +532,8 @@ __global__ __launch_bounds__(256) void gemv_group(GroupArgs g) {
         case 12: gemv_q4k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         case 13: gemv_q4k_body<1, 1, true>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         case 14: gemv_q6k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
+        case 10: gemv_q2k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
+        case 11: gemv_q3k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         default: gemv_q8_0_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
         }
     }
@@ -347,7 +543,8 @@ hipError_t launch_gemv_group(GroupArgs g, hipStream_t s) {
     int total = 0;
     for (int i = 0; i < g.n; i++) {
         GroupProblem &q = g.p[i];
-        if (q.type != 12 && q.type != 13 && q.type != 14 && q.type != 8) return hipErrorInvalidValue;
+        if (q.type != 12 && q.type != 13 && q.type != 14 && q.type != 8 && q.type != 10 && q.type != 11)
+            return hipErrorInvalidValue;
         q.rows_per_wave = q.nrows >= 2048 ? 2 : 1;
         q.wg_begin = total;
         total += (q.nrows + 4 * q.rows_per_wave - 1) / (4 * q.rows_per_wave);
@@ -394,6 +591,8 @@ static hipError_t launch_q(int type, const uint8_t *W, size_t pitch, int nb, int
     case 13: gemv_q5k<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
     case 14: gemv_q6k<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
     case 8: gemv_q8_0<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
+    case 10: gemv_q2k<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
+    case 11: gemv_q3k<R, B><<<grid, block, 0, s>>>(W, pitch, nb, nrows, X, ldx, Y, ldy); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -84,6 +84,46 @@ __device__ __forceinline__ void dequant_q8_0(const uint8_t *__restrict__ W, int6
     for (int i = 0; i < 32; i++) o[i] = __fmul_rn(d, (float)(int8_t)bp[2 + i]);
 }
 
+// dequantizeQ2K (LlamaTransformerHandler.java:915-952): unit t = 16 elements
+// of block t/16, half h = (t/8)&1, group k = t&7: elements h*128 + 16k + l take
+// the 2 bits at shift 2(k/2) of qs[32h + 16(k&1) + l] and scale byte sc[8h + k];
+// w = (d*(sc&15))*q - dmin*(sc>>4).
+__device__ __forceinline__ void dequant_q2k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
+    const int64_t blk = t >> 4;
+    const int h = (int)(t >> 3) & 1, k = (int)t & 7;
+    const uint8_t *bp = W + blk * 84;
+    const float d = half_bits_to_float(bp[80] | (bp[81] << 8)), dmin = half_bits_to_float(bp[82] | (bp[83] << 8));
+    const int sc = bp[8 * h + k];
+    const float dl = __fmul_rn(d, (float)(sc & 15)), ml = __fmul_rn(dmin, (float)(sc >> 4));
+    const uint8_t *qs = bp + 16 + 32 * h + 16 * (k & 1);
+    const int shift = 2 * (k >> 1);
+    float *o = out + blk * 256 + h * 128 + 16 * k;
+    for (int l = 0; l < 16; l++) o[l] = __fsub_rn(__fmul_rn(dl, (float)((qs[l] >> shift) & 3)), ml);
+}
+
+// dequantizeQ3K (LlamaTransformerHandler.java:954-1015): unit t = 16 elements
+// of block t/16, group is = t&15 = 8h + 2j + r: elements h*128 + 32j + 16r + l
+// take the 2 bits at shift 2j of qs[32h + 16r + l] and bit 4h + j of
+// hmask[16r + l]; w = (d*sc[is]) * ((low2 | hi<<2) - 4), exact.
+__device__ __forceinline__ void dequant_q3k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
+    const int64_t blk = t >> 4;
+    const int is = (int)t & 15, h = is >> 3, j = (is >> 1) & 3, r = is & 1;
+    const uint8_t *bp = W + blk * 110;
+    const float d = half_bits_to_float(bp[108] | (bp[109] << 8));
+    // scale is: 4 low bits from byte is&7 (high nibble for is >= 8), 2 high bits
+    // from byte 8 + (is&3) at bit 2*(is/4) (the utmp words of :969-985)
+    const int lo4 = (bp[96 + (is & 7)] >> (is >= 8 ? 4 : 0)) & 15;
+    const int hi2 = (bp[104 + (is & 3)] >> (2 * (is >> 2))) & 3;
+    const float dl = __fmul_rn(d, (float)((lo4 | (hi2 << 4)) - 32));
+    const uint8_t *qs = bp + 32 + 32 * h + 16 * r, *hm = bp + 16 * r;
+    const int m = 1 << (4 * h + j);
+    float *o = out + blk * 256 + h * 128 + 32 * j + 16 * r;
+    for (int l = 0; l < 16; l++) {
+        const int q = (((qs[l] >> (2 * j)) & 3) | ((hm[l] & m) ? 4 : 0)) - 4;
+        o[l] = __fmul_rn(dl, (float)q);
+    }
+}
+
 __device__ __forceinline__ void dequant_f32(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
     out[t] = reinterpret_cast<const float *>(W)[t];
 }
@@ -93,6 +133,8 @@ template <int T> __device__ __forceinline__ void dequant_unit(const uint8_t *W, 
     else if constexpr (T == 13) dequant_q5k(W, t, out);
     else if constexpr (T == 14) dequant_q6k(W, t, out);
     else if constexpr (T == 8) dequant_q8_0(W, t, out);
+    else if constexpr (T == 10) dequant_q2k(W, t, out);
+    else if constexpr (T == 11) dequant_q3k(W, t, out);
     else dequant_f32(W, t, out);
 }
 
@@ -119,7 +161,9 @@ int64_t dequant_units(int type, int64_t n) {
     case 12:
     case 13:
     case 8: return n / 32;
-    case 14: return n / 16;
+    case 14:
+    case 10:
+    case 11: return n / 16;
     case 0: return n;
     default: return -1;
     }
@@ -135,6 +179,8 @@ hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float 
     case 13: dequant_k<13><<<grid, block, 0, s>>>(w, units, out); break;
     case 14: dequant_k<14><<<grid, block, 0, s>>>(w, units, out); break;
     case 8: dequant_k<8><<<grid, block, 0, s>>>(w, units, out); break;
+    case 10: dequant_k<10><<<grid, block, 0, s>>>(w, units, out); break;
+    case 11: dequant_k<11><<<grid, block, 0, s>>>(w, units, out); break;
     case 0: dequant_k<0><<<grid, block, 0, s>>>(w, units, out); break;
     }
     return hipGetLastError();
@@ -150,6 +196,8 @@ hipError_t launch_dequant_row(int type, const uint8_t *w, int rows, int cols, si
     case 13: dequant_row_k<13><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
     case 14: dequant_row_k<14><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
     case 8: dequant_row_k<8><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
+    case 10: dequant_row_k<10><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
+    case 11: dequant_row_k<11><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
     case 0: dequant_row_k<0><<<grid, block, 0, s>>>(w, d_tokens, rows, pitch, units, cols, out); break;
     }
     return hipGetLastError();

@@ -50,10 +50,10 @@ class IOException(OSError):
     pass
 
 
-F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
-SUPPORTED_TYPES = (F32, Q8_0, Q4_K, Q5_K, Q6_K)
-_QK = {F32: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
-_BLOCK_BYTES = {F32: 4, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 8, 10, 11, 12, 13, 14
+SUPPORTED_TYPES = (F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)
+_QK = {F32: 1, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+_BLOCK_BYTES = {F32: 4, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 
 
 def raw_byte_count(qtype: int, nelems: int) -> int:
@@ -70,6 +70,8 @@ class MatVecBackend(enum.Enum):
     ROCM_RESIDENT = "rocm-resident"
     ROCM_RESIDENT_FP16 = "rocm-resident-fp16"
     # new: packed weights resident on the device, fused dequant-GEMV
+    ROCM_RESIDENT_Q2K = "rocm-resident-q2k"
+    ROCM_RESIDENT_Q3K = "rocm-resident-q3k"
     ROCM_RESIDENT_Q4K = "rocm-resident-q4k"
     ROCM_RESIDENT_Q5K = "rocm-resident-q5k"
     ROCM_RESIDENT_Q6K = "rocm-resident-q6k"
@@ -81,7 +83,8 @@ class MatVecBackend(enum.Enum):
 
     @staticmethod
     def for_type(qtype: int) -> "MatVecBackend":
-        return {F32: MatVecBackend.ROCM_RESIDENT, Q4_K: MatVecBackend.ROCM_RESIDENT_Q4K, Q5_K: MatVecBackend.ROCM_RESIDENT_Q5K,
+        return {F32: MatVecBackend.ROCM_RESIDENT, Q2_K: MatVecBackend.ROCM_RESIDENT_Q2K,
+                Q3_K: MatVecBackend.ROCM_RESIDENT_Q3K, Q4_K: MatVecBackend.ROCM_RESIDENT_Q4K, Q5_K: MatVecBackend.ROCM_RESIDENT_Q5K,
                 Q6_K: MatVecBackend.ROCM_RESIDENT_Q6K, Q8_0: MatVecBackend.ROCM_RESIDENT_Q8_0}[qtype]
 
 

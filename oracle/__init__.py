@@ -26,9 +26,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_build", "libjuno_oracle.so")
 
-F32, Q8_0, Q4_K, Q5_K, Q6_K = 0, 8, 12, 13, 14
-QK = {F32: 1, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
-BLOCK_BYTES = {F32: 4, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+F32, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = 0, 8, 10, 11, 12, 13, 14
+QK = {F32: 1, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {F32: 4, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 
 _lib = None
 
@@ -71,6 +71,8 @@ def lib() -> ctypes.CDLL:
         L.or_raw_byte_count.argtypes = [ctypes.c_int, ctypes.c_int64]
         L.or_q4k_scale.argtypes = [P, ctypes.c_int]
         L.or_q4k_min.argtypes = [P, ctypes.c_int]
+        L.or_q3k_scales.argtypes = [P, P]
+        L.or_q3k_scales.restype = None
         L.or_dequantize.argtypes = [ctypes.c_int, P, ctypes.c_int, ctypes.c_int, P]
         L.or_matvec.argtypes = [ctypes.c_int, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                 P, ctypes.c_int]
@@ -117,6 +119,14 @@ def q4k_scale(sc: bytes, j: int) -> int:
 def q4k_min(sc: bytes, j: int) -> int:
     b = np.frombuffer(bytes(sc), dtype=np.uint8).copy()
     return lib().or_q4k_min(_ptr(b), j)
+
+
+def q3k_scales(sc12: bytes) -> list:
+    """The 16 signed Q3_K sub-block scales of a 12-byte field."""
+    b = np.frombuffer(bytes(sc12), dtype=np.uint8).copy()
+    out = np.zeros(16, dtype=np.int32)
+    lib().or_q3k_scales(_ptr(b), _ptr(out))
+    return out.tolist()
 
 
 def _as_u8(raw) -> np.ndarray:

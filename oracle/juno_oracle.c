@@ -116,6 +116,8 @@ int64_t or_raw_byte_count(int type, int64_t nelems) {
     switch (type) {
     case OR_TYPE_F32: return nelems * 4;
     case OR_TYPE_Q8_0: return (nelems / 32) * 34;
+    case OR_TYPE_Q2_K: return (nelems / 256) * 84;
+    case OR_TYPE_Q3_K: return (nelems / 256) * 110;
     case OR_TYPE_Q4_K: return (nelems / 256) * 144;
     case OR_TYPE_Q5_K: return (nelems / 256) * 176;
     case OR_TYPE_Q6_K: return (nelems / 256) * 210;
@@ -143,6 +145,8 @@ static int block_geometry(int type, int *qk, int *bytes) {
     switch (type) {
     case OR_TYPE_F32: *qk = 1; *bytes = 4; return 0;
     case OR_TYPE_Q8_0: *qk = 32; *bytes = 34; return 0;
+    case OR_TYPE_Q2_K: *qk = 256; *bytes = 84; return 0;
+    case OR_TYPE_Q3_K: *qk = 256; *bytes = 110; return 0;
     case OR_TYPE_Q4_K: *qk = 256; *bytes = 144; return 0;
     case OR_TYPE_Q5_K: *qk = 256; *bytes = 176; return 0;
     case OR_TYPE_Q6_K: *qk = 256; *bytes = 210; return 0;
@@ -227,6 +231,62 @@ static void deq_q6_k(const uint8_t *bo, float *out) {
     }
 }
 
+/* dequantizeQ2K (LlamaTransformerHandler.java:915-952): [scales 16][qs 64][d][dmin];
+ * per half of 128, element l + 16k (k = 0..7) uses scale byte 8*half + k (low
+ * nibble scale, high nibble min) and the 2 bits at shift 2*(k/2) of
+ * qs[32*half + l + 16*(k&1)]: out = (d*sc)*q - dmin*m. */
+static void deq_q2_k(const uint8_t *bo, float *out) {
+    float d = or_f16_to_f32(le16(bo + 80)), dmin = or_f16_to_f32(le16(bo + 82));
+    for (int half = 0; half < 2; half++) {
+        const uint8_t *sh = bo + half * 8, *qh = bo + 16 + half * 32;
+        float *o = out + half * 128;
+        for (int l = 0; l < 16; l++) {
+            int q0 = qh[l], q1 = qh[l + 16];
+            for (int k = 0; k < 8; k++) {
+                int q = ((k & 1) ? q1 : q0) >> (2 * (k / 2)) & 3;
+                o[l + 16 * k] = d * (float)(sh[k] & 0x0F) * (float)q - dmin * (float)(sh[k] >> 4);
+            }
+        }
+    }
+}
+
+/* The 16 signed 6-bit scales of a Q3_K block (biased by 32), unpacked from 12
+ * bytes as dequantizeQ3K does (LlamaTransformerHandler.java:969-985). */
+void or_q3k_scales(const uint8_t *sc12, int sc[16]) {
+    uint32_t aux0 = sc12[0] | (sc12[1] << 8) | (sc12[2] << 16) | ((uint32_t)sc12[3] << 24);
+    uint32_t aux1 = sc12[4] | (sc12[5] << 8) | (sc12[6] << 16) | ((uint32_t)sc12[7] << 24);
+    uint32_t aux2 = sc12[8] | (sc12[9] << 8) | (sc12[10] << 16) | ((uint32_t)sc12[11] << 24);
+    uint32_t utmp[4] = {(aux0 & 0x0f0f0f0fu) | ((aux2 & 0x03030303u) << 4),
+                        (aux1 & 0x0f0f0f0fu) | (((aux2 >> 2) & 0x03030303u) << 4),
+                        ((aux0 >> 4) & 0x0f0f0f0fu) | (((aux2 >> 4) & 0x03030303u) << 4),
+                        ((aux1 >> 4) & 0x0f0f0f0fu) | (((aux2 >> 6) & 0x03030303u) << 4)};
+    for (int k = 0; k < 4; k++)
+        for (int j = 0; j < 4; j++) sc[4 * k + j] = (int)((utmp[k] >> (8 * j)) & 0xFF) - 32;
+}
+
+/* dequantizeQ3K (LlamaTransformerHandler.java:954-1015): [hmask 32][qs 64][scales 12][d];
+ * group is = 2j + r of half h (16 elements l) takes the 2 bits at shift 2j of
+ * qs[32h + 16r + l] and bit (4h + j) of hmask[16r + l] as q = (low2 | hi<<2) - 4;
+ * out = (d*sc[is]) * q (exact). */
+static void deq_q3_k(const uint8_t *bo, float *out) {
+    const uint8_t *hm = bo, *qs = bo + 32;
+    float d = or_f16_to_f32(le16(bo + 108));
+    int sc[16];
+    or_q3k_scales(bo + 96, sc);
+    int is = 0, m = 1, oi = 0;
+    for (int half = 0; half < 2; half++) {
+        const uint8_t *qh = qs + half * 32;
+        for (int j = 0, shift = 0; j < 4; j++, shift += 2, m <<= 1)
+            for (int r = 0; r < 2; r++) {
+                float dl = d * (float)sc[is++];
+                for (int l = 0; l < 16; l++) {
+                    int low2 = (qh[16 * r + l] >> shift) & 3, hi = (hm[16 * r + l] & m) ? 4 : 0;
+                    out[oi++] = dl * (float)((low2 | hi) - 4);
+                }
+            }
+    }
+}
+
 static void deq_f32(const uint8_t *bo, float *out) { memcpy(out, bo, 4); } /* dequantizeF32 :887-893 */
 
 typedef void (*deq_fn)(const uint8_t *, float *);
@@ -235,6 +295,8 @@ static deq_fn deq_for(int type) {
     switch (type) {
     case OR_TYPE_F32: return deq_f32;
     case OR_TYPE_Q8_0: return deq_q8_0;
+    case OR_TYPE_Q2_K: return deq_q2_k;
+    case OR_TYPE_Q3_K: return deq_q3_k;
     case OR_TYPE_Q4_K: return deq_q4_k;
     case OR_TYPE_Q5_K: return deq_q5_k;
     case OR_TYPE_Q6_K: return deq_q6_k;
@@ -372,12 +434,65 @@ static float row_q6_k(const uint8_t *row, const float *x, int cols) {
     return acc;
 }
 
+/* matVecQ2Kraw (LlamaTransformerHandler.java:1303-1346): per half and l, the
+ * eight terms l + 16k (k = 0..7) in that order, each ((d*sc)*q - dmin*m) * x. */
+static float row_q2_k(const uint8_t *row, const float *x, int cols) {
+    float acc = 0.0f;
+    int nb = cols / 256;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *bo = row + (size_t)b * 84;
+        float d = or_f16_to_f32(le16(bo + 80)), dmin = or_f16_to_f32(le16(bo + 82));
+        for (int half = 0; half < 2; half++) {
+            const uint8_t *sh = bo + half * 8, *qh = bo + 16 + half * 32;
+            const float *xo = x + b * 256 + half * 128;
+            for (int l = 0; l < 16; l++) {
+                int q0 = qh[l], q1 = qh[l + 16];
+                for (int k = 0; k < 8; k++) {
+                    int q = ((k & 1) ? q1 : q0) >> (2 * (k / 2)) & 3;
+                    acc += (d * (float)(sh[k] & 0x0F) * (float)q - dmin * (float)(sh[k] >> 4)) * xo[l + 16 * k];
+                }
+            }
+        }
+    }
+    return acc;
+}
+
+/* matVecQ3Kraw (LlamaTransformerHandler.java:1358-1425): elements in order,
+ * acc += ((d*sc)*q) * x. */
+static float row_q3_k(const uint8_t *row, const float *x, int cols) {
+    float acc = 0.0f;
+    int nb = cols / 256;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t *bo = row + (size_t)b * 110;
+        const uint8_t *hm = bo, *qs = bo + 32;
+        float d = or_f16_to_f32(le16(bo + 108));
+        int sc[16];
+        or_q3k_scales(bo + 96, sc);
+        const float *xb = x + b * 256;
+        int is = 0, m = 1, xi = 0;
+        for (int half = 0; half < 2; half++) {
+            const uint8_t *qh = qs + half * 32;
+            for (int j = 0, shift = 0; j < 4; j++, shift += 2, m <<= 1)
+                for (int r = 0; r < 2; r++) {
+                    float dl = d * (float)sc[is++];
+                    for (int l = 0; l < 16; l++) {
+                        int low2 = (qh[16 * r + l] >> shift) & 3, hi = (hm[16 * r + l] & m) ? 4 : 0;
+                        acc += dl * (float)((low2 | hi) - 4) * xb[xi++];
+                    }
+                }
+        }
+    }
+    return acc;
+}
+
 typedef float (*row_fn)(const uint8_t *, const float *, int);
 
 static row_fn row_for(int type) {
     switch (type) {
     case OR_TYPE_F32: return row_f32;
     case OR_TYPE_Q8_0: return row_q8_0;
+    case OR_TYPE_Q2_K: return row_q2_k;
+    case OR_TYPE_Q3_K: return row_q3_k;
     case OR_TYPE_Q4_K: return row_q4_k;
     case OR_TYPE_Q5_K: return row_q5_k;
     case OR_TYPE_Q6_K: return row_q6_k;

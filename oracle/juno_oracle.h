@@ -26,6 +26,8 @@ extern "C" {
 enum {
     OR_TYPE_F32 = 0,
     OR_TYPE_Q8_0 = 8,
+    OR_TYPE_Q2_K = 10,
+    OR_TYPE_Q3_K = 11,
     OR_TYPE_Q4_K = 12,
     OR_TYPE_Q5_K = 13,
     OR_TYPE_Q6_K = 14,
@@ -40,6 +42,8 @@ int64_t  or_raw_byte_count(int type, int64_t nelems);
 /* Q4_K 6-bit scale / min unpack for sub-block j (0..7) of the 12 scale bytes. */
 int or_q4k_scale(const uint8_t *sc, int j);
 int or_q4k_min(const uint8_t *sc, int j);
+/* The 16 signed Q3_K sub-block scales (dequantizeQ3K, LlamaTransformerHandler.java:969-985). */
+void or_q3k_scales(const uint8_t *sc12, int sc[16]);
 
 /* Dequantize rows*cols elements of a packed tensor to fp32 (row-major).
  * Returns 0, or -1 for an unsupported type / cols not a block multiple. */

@@ -50,11 +50,12 @@ def test_raw_byte_count_matches_reference_formula():
     L = _lib.load()
     out = ctypes.c_int64()
     # GgufReader.rawByteCount (GgufReader.java:347-360)
-    for t, n, want in [(12, 256 * 32, 32 * 144), (14, 256, 210), (8, 32, 34), (0, 10, 40)]:
+    for t, n, want in [(12, 256 * 32, 32 * 144), (14, 256, 210), (8, 32, 34), (0, 10, 40), (10, 256, 84),
+                       (11, 512, 220), (13, 256, 176)]:
         assert L.jh_raw_byte_count(t, n, ctypes.byref(out)) == 0
         assert out.value == want
-    assert L.jh_raw_byte_count(10, 256, ctypes.byref(out)) == _lib.JH_EUNSUPPORTED
-    assert "GGML type 10" in _lib.last_error()
+    assert L.jh_raw_byte_count(99, 256, ctypes.byref(out)) == _lib.JH_EUNSUPPORTED
+    assert "GGML type 99" in _lib.last_error()
 
 
 def test_ctx_create_without_device_reports_enodev():

@@ -103,10 +103,10 @@ def test_reference_known_answer_blocks_through_a_file(be, tmp_path, golden):
 
 def test_upload_errors(be, tmp_path):
     p = tmp_path / "e.gguf"
-    p.write_bytes(gguf_bytes((), [("q2", [256], 10, bytes(84)), ("odd", [100, 2], 12, bytes(0))]))
+    p.write_bytes(gguf_bytes((), [("q40", [256], 2, bytes(144)), ("odd", [100, 2], 12, bytes(0))]))
     with GgufReader.open(p) as r:
         with pytest.raises(UnsupportedOperationException):
-            r.upload("q2", be)  # Q2_K is not a device format (yet)
+            r.upload("q40", be)  # Q4_0: sized by rawByteCount, but the reference has no matVec for it
         with pytest.raises(Exception, match="multiple of the block size"):
             r.upload("odd", be)
 

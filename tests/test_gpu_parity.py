@@ -347,7 +347,7 @@ def test_argument_errors(be):
     with pytest.raises(mv.IllegalArgumentException, match="cols"):
         be.upload_quant(O.Q4_K, 1, 300, np.zeros(144, np.uint8))
     with pytest.raises(mv.UnsupportedOperationException):
-        be.upload_quant(10, 1, 256, np.zeros(84, np.uint8))
+        be.upload_quant(2, 1, 256, np.zeros(144, np.uint8))  # Q4_0: sized by rawByteCount, no matVec
     dev = upload(be, O.Q4_K, raw, rows, cols)
     with pytest.raises(mv.IllegalArgumentException, match="cols"):
         be.sgemv_quant(dev, np.zeros(cols + 1, np.float32))
