@@ -216,6 +216,14 @@ int jh_embed_dev(const jh_qmat *m, const int *d_token, float *d_out, void *strea
 /* jh_embed_dev for n tokens d_tokens[0..n) into d_out[n][cols] (a batch of requests). */
 int jh_embed_rows_dev(const jh_qmat *m, const int *d_tokens, int n, float *d_out, void *stream);
 
+/* LoRA overlay: for each of `batch` rows, d_y[b][0..out_dim) += scale * B (A d_x[b]), with
+ * A [rank][in_dim] and B [out_dim][rank] fp32 in HBM.  LoraAdapter.forward
+ * (lora/.../LoraAdapter.java:79-98) added to a projection's output as
+ * LoraTrainableHandler.applyLoraInPlace does (LoraTrainableHandler.java:475-476, 489-496);
+ * scale = alpha / rank.  Uses the stream workspace for the rank-r intermediate. */
+int jh_lora_apply_dev(const float *d_a, const float *d_b, int rank, int in_dim, int out_dim, float scale,
+                      const float *d_x, int batch, float *d_y, void *stream);
+
 /* *d_pos += delta, on the device (for replaying a captured decode step). */
 int jh_pos_increment_dev(int *d_pos, int delta, void *stream);
 

@@ -689,6 +689,23 @@ int jh_silu_mul_dev(const float *gate, const float *up, int n, float *out, void 
     return ok();
 }
 
+int jh_lora_apply_dev(const float *d_a, const float *d_b, int rank, int in_dim, int out_dim, float scale,
+                      const float *d_x, int batch, float *d_y, void *stream) {
+    if (rank < 1 || rank > 4096) return fail(JH_EINVAL, "rank=%d outside [1, 4096]", rank);
+    if (in_dim < 1 || out_dim < 1) return fail(JH_EINVAL, "inDim=%d and outDim=%d must be >= 1", in_dim, out_dim);
+    if (batch < 0 || batch > 65535) return fail(JH_EINVAL, "batch=%d outside [0, 65535]", batch);
+    if (batch == 0) return ok();
+    if (!d_a || !d_b || !d_x || !d_y) return fail(JH_EINVAL, "pointers must not be null");
+    int dev = 0, rc;
+    JH_HIP("hipGetDevice", hipGetDevice(&dev));
+    void *ws = nullptr;
+    if ((rc = stream_workspace(dev, (hipStream_t)stream, (size_t)batch * rank * sizeof(float), &ws))) return rc;
+    hipError_t e = jh::launch_lora(d_a, d_b, rank, in_dim, out_dim, scale, d_x, batch, d_y, static_cast<float *>(ws),
+                                   (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("lora launch", e);
+    return ok();
+}
+
 int jh_pos_increment_dev(int *d_pos, int delta, void *stream) {
     if (!d_pos) return fail(JH_EINVAL, "d_pos must not be null");
     hipError_t e = jh::launch_pos_increment(d_pos, delta, (hipStream_t)stream);

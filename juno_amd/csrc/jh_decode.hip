@@ -270,6 +270,35 @@ __global__ __launch_bounds__(256) void silu_mul_k(const float *__restrict__ gate
     }
 }
 
+// ------------------------------------------------------------------ LoRA overlay
+// LoraAdapter.forward (LoraAdapter.java:79-98): h = A x (A [rank][in]), then
+// delta = (B h) * scale (B [out][rank]); applyLoraInPlace adds delta to the
+// projection's output (LoraTrainableHandler.java:489-496).  One workgroup per
+// (r, request) for h; one thread per (output row, request) for the update.
+__global__ __launch_bounds__(256) void lora_down_k(const float *__restrict__ A, const float *__restrict__ x, int in_dim,
+                                                   int rank, float *__restrict__ h) {
+    __shared__ float part[4];
+    const int r = blockIdx.x, b = blockIdx.y;
+    const float *ar = A + (size_t)r * in_dim, *xb = x + (size_t)b * in_dim;
+    float acc = 0.f;
+    for (int c = threadIdx.x; c < in_dim; c += 256) acc += ar[c] * xb[c];
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) h[(size_t)b * rank + r] = (part[0] + part[1]) + (part[2] + part[3]);
+}
+
+__global__ __launch_bounds__(256) void lora_up_k(const float *__restrict__ B, const float *__restrict__ h, int rank,
+                                                 int out_dim, float scale, float *__restrict__ y) {
+    const int i = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
+    if (i >= out_dim) return;
+    const float *br = B + (size_t)i * rank, *hb = h + (size_t)b * rank;
+    float acc = 0.f;
+    for (int c = 0; c < rank; c++) acc += br[c] * hb[c];
+    float *yp = y + (size_t)b * out_dim + i;
+    *yp = *yp + acc * scale;
+}
+
 __global__ void pos_increment_k(int *d_pos, int delta) {
     if (threadIdx.x == 0) *d_pos += delta;
 }
@@ -329,6 +358,15 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
 
 hipError_t launch_silu_mul(const float *gate, const float *up, int n, float *out, hipStream_t s) {
     silu_mul_k<<<(n + 255) / 256, 256, 0, s>>>(gate, up, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_lora(const float *a, const float *b, int rank, int in_dim, int out_dim, float scale, const float *x,
+                       int batch, float *y, float *h_ws, hipStream_t s) {
+    lora_down_k<<<dim3(rank, batch), 256, 0, s>>>(a, x, in_dim, rank, h_ws);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    lora_up_k<<<dim3((out_dim + 255) / 256, batch), 256, 0, s>>>(b, h_ws, rank, out_dim, scale, y);
     return hipGetLastError();
 }
 

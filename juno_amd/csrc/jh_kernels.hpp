@@ -88,6 +88,9 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
                             bool fused, float *out, void *workspace, hipStream_t s, int batch = 1,
                             const int *d_slot = nullptr, int n_slots = 1);
 hipError_t launch_silu_mul(const float *gate, const float *up, int n, float *out, hipStream_t s);
+// y[b] += scale * B (A x[b]) for b < batch; h_ws holds batch * rank floats.
+hipError_t launch_lora(const float *a, const float *b, int rank, int in_dim, int out_dim, float scale, const float *x,
+                       int batch, float *y, float *h_ws, hipStream_t s);
 hipError_t launch_pos_increment(int *d_pos, int delta, hipStream_t s);
 
 }  // namespace jh

@@ -245,9 +245,10 @@ class LlamaDecoder:
     """One request's decode state: KV cache [layers][max_seq][kv_dim] in HBM,
     activation buffers and the device position."""
 
-    def __init__(self, weights: LlamaWeights, max_seq: int, device: int = 0):
+    def __init__(self, weights: LlamaWeights, max_seq: int, device: int = 0, lora=None):
         torch = _torch()
         self.w, self.cfg, self.max_seq = weights, weights.cfg, max_seq
+        self.lora = lora  # LoraAdapterSet: "wq" / "wv" deltas after the Q and V projections
         c = self.cfg
         self.L = _lib.load()
         dev = torch.device("cuda", device)
@@ -297,6 +298,11 @@ class LlamaDecoder:
                 _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(lw.attn_norm), H, eps, P(self.x), P(self.xn), s))
             m = lw.mats
             self._group([m["q"], m["k"], m["v"]], [self.xn] * 3, [self.q, self.k, self.v], s)
+            if self.lora is not None:  # applyLoraInPlace (LoraTrainableHandler.java:475-476)
+                for proj, out in (("wq", self.q), ("wv", self.v)):
+                    ad = self.lora.get(li, proj)
+                    if ad is not None:
+                        ad.apply_dev(self.xn.data_ptr(), out.data_ptr(), 1, stream)
             # rope on q and k, KV append and gqa (:765-773) in one launch pair
             _check(L.jh_rope_attention_dev(P(self.q), P(self.k), P(self.v), nh, nkv, hd, P(self.pos), self.max_seq,
                                            c.rope_theta, P(self.k_cache[li]), P(self.v_cache[li]), P(self.att), s))

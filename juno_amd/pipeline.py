@@ -14,6 +14,8 @@ Mirrors the reference's pipeline contract (paths under
   B = 16; one batched rope + KV-append + attention launch pair)
 * ``vocab_size()``  InferencePipeline.vocabSize (:71-75)
 * ``evict(request_id)``  LlamaTransformerHandler.evict (:496-504)
+* ``lora``  an optional LoraAdapterSet whose "wq" / "wv" adapters are added after
+  the Q and V projections (LoraTrainableHandler.java:475-476)
 
 KV caches are one slot per live request in [layers][slots][max_seq][kv_dim]
 HBM arrays; a slot is zeroed when a request takes it (the reference allocates
@@ -41,13 +43,14 @@ class LlamaBatchPipeline:
     """A node holding every layer, the embeddings and the output projection."""
 
     def __init__(self, weights: LlamaWeights, max_seq: int, max_batch: int = 64, max_requests: int | None = None,
-                 device: int = 0):
+                 device: int = 0, lora=None):
         torch = _torch()
         if weights.token_embd is None:
             raise IllegalStateException("token input needs token_embd.weight on the device")
         if max_batch < 1 or max_batch > 4096:
             raise IllegalArgumentException(f"max_batch={max_batch} outside [1, 4096]")
         self.w, self.cfg, self.max_seq, self.max_batch = weights, weights.cfg, max_seq, max_batch
+        self.lora = lora  # LoraAdapterSet: "wq" / "wv" deltas after the Q and V projections
         self.n_slots = max_requests or max_batch
         c = self.cfg
         self.L = _lib.load()
@@ -149,6 +152,11 @@ class LlamaBatchPipeline:
             gemv(m["q"], self.xn, self.q)
             gemv(m["k"], self.xn, self.k)
             gemv(m["v"], self.xn, self.v)
+            if self.lora is not None:  # applyLoraInPlace (LoraTrainableHandler.java:475-476)
+                for proj, out in (("wq", self.q), ("wv", self.v)):
+                    ad = self.lora.get(li, proj)
+                    if ad is not None:
+                        ad.apply_dev(self.xn.data_ptr(), out.data_ptr(), B, stream)
             _check(L.jh_rope_attention_batched_dev(P(self.q), P(self.k), P(self.v), B, c.num_heads, c.num_kv_heads,
                                                    c.head_dim, P(self.meta[1]), P(self.meta[2]), self.n_slots,
                                                    self.max_seq, c.rope_theta, P(self.k_cache[li]),

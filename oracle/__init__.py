@@ -86,6 +86,8 @@ def lib() -> ctypes.CDLL:
         L.or_silu.restype = F
         L.or_silu_mul.argtypes = [P, P, I, P]
         L.or_add.argtypes = [P, P, I, P]
+        L.or_lora_forward.argtypes = [P, P, I, I, I, ctypes.c_float, P, P]
+        L.or_lora_forward.restype = None
         L.or_llama_layer.argtypes = [ctypes.POINTER(LlamaLayerC), ctypes.POINTER(LlamaDimsC), P, I, P, P, I]
         _lib = L
     return _lib
@@ -212,6 +214,16 @@ def silu_mul(gate, up) -> np.ndarray:
     gate, up = _f32(gate), _f32(up)
     out = np.empty_like(gate)
     lib().or_silu_mul(_ptr(gate), _ptr(up), gate.size, _ptr(out))
+    return out
+
+
+def lora_forward(a, b, rank: int, in_dim: int, out_dim: int, scale: float, x) -> np.ndarray:
+    """LoraAdapter.forward: (B (A x)) * scale in the reference's summation order."""
+    a, b, x = _f32(a), _f32(b), _f32(x)
+    if a.size != rank * in_dim or b.size != out_dim * rank or x.size != in_dim or rank > 4096:
+        raise ValueError("lora_forward: shape mismatch")
+    out = np.empty(out_dim, dtype=np.float32)
+    lib().or_lora_forward(_ptr(a), _ptr(b), rank, in_dim, out_dim, scale, _ptr(x), _ptr(out))
     return out
 
 

@@ -67,6 +67,9 @@ void  or_gqa(const float *q, const float *k_cache, const float *v_cache, int n_h
              int head_dim, int seq_len, float *out);
 float or_silu(float x);
 void  or_silu_mul(const float *gate, const float *up, int n, float *out);
+/* LoraAdapter.forward: delta = (B (A x)) * scale, rank <= 4096. */
+void  or_lora_forward(const float *a, const float *b, int rank, int in_dim, int out_dim, float scale, const float *x,
+                      float *delta);
 void  or_add(const float *a, const float *b, int n, float *out);
 
 typedef struct {

@@ -90,6 +90,24 @@ void or_silu_mul(const float *gate, const float *up, int n, float *out) {
 }
 
 /* add, LlamaTransformerHandler.java:1737-1742 */
+/* LoraAdapter.forward (lora/src/main/java/cab/ml/juno/lora/LoraAdapter.java:79-98):
+ * h[r] = sum_c a[r*in + c] * x[c] in c order; delta[o] = (sum_r b[o*rank + r] * h[r]) * scale. */
+void or_lora_forward(const float *a, const float *b, int rank, int in_dim, int out_dim, float scale, const float *x,
+                     float *delta) {
+    float h[4096];
+    if (rank > 4096) return;
+    for (int r = 0; r < rank; r++) {
+        float acc = 0.0f;
+        for (int c = 0; c < in_dim; c++) acc += a[(size_t)r * in_dim + c] * x[c];
+        h[r] = acc;
+    }
+    for (int o = 0; o < out_dim; o++) {
+        float acc = 0.0f;
+        for (int c = 0; c < rank; c++) acc += b[(size_t)o * rank + c] * h[c];
+        delta[o] = acc * scale;
+    }
+}
+
 void or_add(const float *a, const float *b, int n, float *out) {
     for (int i = 0; i < n; i++) out[i] = a[i] + b[i];
 }
