@@ -216,6 +216,11 @@ int jh_embed_dev(const jh_qmat *m, const int *d_token, float *d_out, void *strea
 /* jh_embed_dev for n tokens d_tokens[0..n) into d_out[n][cols] (a batch of requests). */
 int jh_embed_rows_dev(const jh_qmat *m, const int *d_tokens, int n, float *d_out, void *stream);
 
+/* d_y[r][i] += d_bias[i] for each of rows rows of n: the Q / K / V projection biases of
+ * Qwen2-style models, added right after the projections (addInPlace,
+ * LlamaTransformerHandler.java:758-761, 1641-1646). */
+int jh_add_rows_dev(float *d_y, const float *d_bias, int n, int rows, void *stream);
+
 /* LoRA overlay: for each of `batch` rows, d_y[b][0..out_dim) += scale * B (A d_x[b]), with
  * A [rank][in_dim] and B [out_dim][rank] fp32 in HBM.  LoraAdapter.forward
  * (lora/.../LoraAdapter.java:79-98) added to a projection's output as

@@ -47,6 +47,7 @@ SIGNATURES = {
     "jh_pos_increment_dev": (_I, [_P, _I, _P]),
     "jh_embed_dev": (_I, [_P, _P, _P, _P]),
     "jh_embed_rows_dev": (_I, [_P, _P, _I, _P, _P]),
+    "jh_add_rows_dev": (_I, [_P, _P, _I, _I, _P]),
     "jh_lora_apply_dev": (_I, [_P, _P, _I, _I, _I, ctypes.c_float, _P, _I, _P, _P]),
     "jh_rmsnorm_rows_dev": (_I, [_P, _P, _P, _I, _I, ctypes.c_float, _P, _P, _P]),
     "jh_rope_attention_batched_dev": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _I, ctypes.c_float, _P, _P, _P,

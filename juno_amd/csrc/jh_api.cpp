@@ -689,6 +689,15 @@ int jh_silu_mul_dev(const float *gate, const float *up, int n, float *out, void 
     return ok();
 }
 
+int jh_add_rows_dev(float *d_y, const float *d_bias, int n, int rows, void *stream) {
+    if (n < 0 || rows < 0 || rows > 65535) return fail(JH_EINVAL, "n=%d and rows=%d must be >= 0 (rows <= 65535)", n, rows);
+    if (n == 0 || rows == 0) return ok();
+    if (!d_y || !d_bias) return fail(JH_EINVAL, "pointers must not be null");
+    hipError_t e = jh::launch_add_rows(d_y, d_bias, n, rows, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail("add_rows launch", e);
+    return ok();
+}
+
 int jh_lora_apply_dev(const float *d_a, const float *d_b, int rank, int in_dim, int out_dim, float scale,
                       const float *d_x, int batch, float *d_y, void *stream) {
     if (rank < 1 || rank > 4096) return fail(JH_EINVAL, "rank=%d outside [1, 4096]", rank);

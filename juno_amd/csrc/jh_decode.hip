@@ -299,6 +299,16 @@ __global__ __launch_bounds__(256) void lora_up_k(const float *__restrict__ B, co
     *yp = *yp + acc * scale;
 }
 
+// addInPlace (LlamaTransformerHandler.java:1641-1646) on each of rows rows:
+// y[r][i] += bias[i] (the Q / K / V projection biases, :758-761).
+__global__ __launch_bounds__(256) void add_rows_k(float *__restrict__ y, const float *__restrict__ bias, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) {
+        float *yr = y + (size_t)blockIdx.y * n;
+        yr[i] = yr[i] + bias[i];
+    }
+}
+
 __global__ void pos_increment_k(int *d_pos, int delta) {
     if (threadIdx.x == 0) *d_pos += delta;
 }
@@ -367,6 +377,11 @@ hipError_t launch_lora(const float *a, const float *b, int rank, int in_dim, int
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     lora_up_k<<<dim3((out_dim + 255) / 256, batch), 256, 0, s>>>(b, h_ws, rank, out_dim, scale, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rows(float *y, const float *bias, int n, int rows, hipStream_t s) {
+    add_rows_k<<<dim3((n + 255) / 256, rows), 256, 0, s>>>(y, bias, n);
     return hipGetLastError();
 }
 

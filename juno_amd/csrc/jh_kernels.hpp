@@ -91,6 +91,8 @@ hipError_t launch_silu_mul(const float *gate, const float *up, int n, float *out
 // y[b] += scale * B (A x[b]) for b < batch; h_ws holds batch * rank floats.
 hipError_t launch_lora(const float *a, const float *b, int rank, int in_dim, int out_dim, float scale, const float *x,
                        int batch, float *y, float *h_ws, hipStream_t s);
+// y[r][i] += bias[i] for r < rows, i < n.
+hipError_t launch_add_rows(float *y, const float *bias, int n, int rows, hipStream_t s);
 hipError_t launch_pos_increment(int *d_pos, int delta, hipStream_t s);
 
 }  // namespace jh

@@ -28,7 +28,7 @@ import numpy as np
 
 from . import _lib
 from .matvec import (Q4_K, Q6_K, DeviceQuantMatrix, GpuContext, IllegalArgumentException, IllegalStateException,
-                     UnsupportedOperationException, _check)
+                     _check)
 
 _V = ctypes.c_void_p
 
@@ -112,6 +112,7 @@ class LlamaLayerWeights:
     attn_norm: object  # torch float32 [hidden] on the device
     ffn_norm: object
     mats: dict          # name -> DeviceQuantMatrix
+    bias: dict | None = None  # "q" / "k" / "v" -> torch float32 projection bias (Qwen2), or None
 
 
 @dataclass
@@ -140,14 +141,13 @@ class LlamaWeights:
         """Every layer of a GGUF model, streamed from the file into HBM packed
         (LlamaTransformerHandler.java:238-280, 459-470): blk.N.attn_norm /
         ffn_norm (F32 / F16 / BF16, widened on the host), the seven projections,
+        the Q / K / V biases when the file has them (Qwen2, :258-280),
         output_norm, output.weight (token_embd.weight when the embeddings are
         tied) and token_embd.weight for token input."""
         torch = _torch()
         cfg = cfg or LlamaConfig.from_gguf(r)
         cfg.validate()
-        if cfg.num_layers > 0 and r.has_tensor("blk.0.attn_q.bias"):
-            raise UnsupportedOperationException(
-                "Q/K/V projection biases (LlamaTransformerHandler.java:258-280) are not on the device path")
+        has_bias = cfg.num_layers > 0 and r.has_tensor("blk.0.attn_q.bias")  # (LlamaTransformerHandler.java:258)
         be = GpuContext.shared(device).create_mat_vec()
         dev = torch.device("cuda", device)
         vec = lambda name: torch.from_numpy(np.ascontiguousarray(r.tensor(name), dtype=np.float32)).to(dev)
@@ -166,8 +166,9 @@ class LlamaWeights:
             layers = []
             for i in range(cfg.num_layers):
                 mats = {m: mat(f"blk.{i}.{cls.GGUF_NAMES[m]}.weight", *shapes[m]) for m in shapes}
+                bias = {m: vec(f"blk.{i}.attn_{m}.bias") for m in ("q", "k", "v")} if has_bias else None
                 layers.append(LlamaLayerWeights(vec(f"blk.{i}.attn_norm.weight"), vec(f"blk.{i}.ffn_norm.weight"),
-                                                mats))
+                                                mats, bias))
             embd = mat("token_embd.weight", cfg.vocab_size, cfg.hidden_dim) if r.has_tensor("token_embd.weight") \
                 else None
             if r.has_tensor("output.weight"):
@@ -298,6 +299,9 @@ class LlamaDecoder:
                 _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(lw.attn_norm), H, eps, P(self.x), P(self.xn), s))
             m = lw.mats
             self._group([m["q"], m["k"], m["v"]], [self.xn] * 3, [self.q, self.k, self.v], s)
+            if lw.bias is not None:  # addInPlace of the projection biases (:758-761)
+                for name, out in (("q", self.q), ("k", self.k), ("v", self.v)):
+                    _check(L.jh_add_rows_dev(P(out), P(lw.bias[name]), out.numel(), 1, s))
             if self.lora is not None:  # applyLoraInPlace (LoraTrainableHandler.java:475-476)
                 for proj, out in (("wq", self.q), ("wv", self.v)):
                     ad = self.lora.get(li, proj)

@@ -152,6 +152,9 @@ class LlamaBatchPipeline:
             gemv(m["q"], self.xn, self.q)
             gemv(m["k"], self.xn, self.k)
             gemv(m["v"], self.xn, self.v)
+            if lw.bias is not None:  # addInPlace of the projection biases (LlamaTransformerHandler.java:758-761)
+                for name, out, n in (("q", self.q, H), ("k", self.k, KV), ("v", self.v, KV)):
+                    _check(L.jh_add_rows_dev(P(out), P(lw.bias[name]), n, B, s))
             if self.lora is not None:  # applyLoraInPlace (LoraTrainableHandler.java:475-476)
                 for proj, out in (("wq", self.q), ("wv", self.v)):
                     ad = self.lora.get(li, proj)

@@ -18,7 +18,7 @@ import oracle as O
 from gguf_build import (ARRAY, BOOL, FLOAT32, FLOAT64, INT8, INT16, INT32, INT64, STRING, UINT8, UINT16, UINT32,
                         UINT64, big_stub_llamafile, f32_bytes, gguf_bytes, llamafile, minimal_gguf, zip64_llamafile)
 from juno_amd import GgufArray, GgufReader, IllegalArgumentException, IOException, UnsupportedOperationException
-from juno_amd.decode import LlamaConfig, LlamaWeights
+from juno_amd.decode import LlamaConfig
 
 
 def write(tmp_path, name, data: bytes):
@@ -278,13 +278,3 @@ def test_llama_config_from_gguf_llama_fallbacks_and_defaults(tmp_path):
         c = LlamaConfig.from_gguf(r)
     assert (c.hidden_dim, c.num_layers, c.num_heads, c.num_kv_heads, c.intermediate_size, c.vocab_size,
             c.architecture) == (2048, 22, 32, 32, 5632, 32000, "llama")
-
-
-def test_biased_models_are_refused(tmp_path):  # before any device work
-    data = gguf_bytes([("llama.block_count", UINT32, 1), ("llama.embedding_length", UINT32, 256),
-                       ("llama.attention.head_count", UINT32, 4)],
-                      [("blk.0.attn_q.bias", [256], 0, bytes(1024))])
-    p = tmp_path / "b.gguf"
-    p.write_bytes(data)
-    with GgufReader.open(p) as r, pytest.raises(UnsupportedOperationException, match="biases"):
-        LlamaWeights.from_gguf(r)

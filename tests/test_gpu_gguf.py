@@ -137,9 +137,10 @@ CFG = D.LlamaConfig(hidden_dim=256, num_layers=2, num_heads=4, num_kv_heads=2, h
                     vocab_size=1000)
 
 
-def model_gguf(cfg, seed, tied=False, extra_tokens=0):
-    """A GGUF model (Q4_K_M assignment) with llama.* metadata; returns the file
-    bytes and the host tensors for the oracle."""
+def model_gguf(cfg, seed, tied=False, extra_tokens=0, bias=False):
+    """A GGUF model (Q4_K_M assignment) with llama.* metadata, optionally with
+    Q / K / V biases (Qwen2); returns the file bytes and the host tensors for
+    the oracle."""
     rng = np.random.default_rng(seed)
     shapes = D.matrix_shapes(cfg)
     tensors, layers = [], []
@@ -153,6 +154,10 @@ def model_gguf(cfg, seed, tied=False, extra_tokens=0):
             lw["w" + m], lw["type_" + m] = O.quantize(t, f32(rng.standard_normal(rows * cols) * 0.02)), t
             tensors.append((f"blk.{i}.{D.LlamaWeights.GGUF_NAMES[m]}.weight", [cols, rows], t, lw["w" + m].tobytes()))
         tensors.append((f"blk.{i}.ffn_norm.weight", [cfg.hidden_dim], 0, lw["ffn_norm"].tobytes()))
+        if bias:
+            for m, n in (("q", cfg.hidden_dim), ("k", cfg.kv_dim), ("v", cfg.kv_dim)):
+                lw["b" + m] = f32(rng.standard_normal(n) * 0.5)
+                tensors.append((f"blk.{i}.attn_{m}.bias", [n], 0, lw["b" + m].tobytes()))
         layers.append(lw)
     out_norm = f32(1 + 0.1 * rng.standard_normal(cfg.hidden_dim))
     embd = O.quantize(O.Q6_K, f32(rng.standard_normal(cfg.vocab_size * cfg.hidden_dim)))
@@ -227,4 +232,49 @@ def test_token_graph_replay_matches_eager(tmp_path):
             g.replay()
         s.synchronize()
         assert np.array_equal(graph.logits.cpu().numpy(), ref), pos
+    w.close()
+
+
+def oracle_logits_bias(cfg, layers, out_norm, out_raw, x, pos, kc, vc):
+    """transformerLayer with the projection biases (LlamaTransformerHandler.java:743-800,
+    addInPlace :758-761) composed from the oracle's pieces."""
+    nh, nkv, hd, eps = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.rms_norm_eps
+    mv = lambda lw, m, v: O.matvec(lw["type_" + m], lw["w" + m], v, 0, *D.matrix_shapes(cfg)[m])
+    for li, lw in enumerate(layers):
+        xn = O.rmsnorm(x, lw["attn_norm"], eps)
+        q, k, v = (O.add(mv(lw, m, xn), lw["b" + m]) for m in ("q", "k", "v"))
+        q, k = O.rope(q, pos, nh, hd, cfg.rope_theta), O.rope(k, pos, nkv, hd, cfg.rope_theta)
+        kc[li][pos], vc[li][pos] = k, v
+        x2 = O.add(x, mv(lw, "o", O.gqa(q, kc[li], vc[li], nh, nkv, hd, pos + 1)))
+        xn2 = O.rmsnorm(x2, lw["ffn_norm"], eps)
+        x = O.add(x2, mv(lw, "down", O.silu_mul(mv(lw, "gate", xn2), mv(lw, "up", xn2))))
+    return O.matvec(O.Q6_K, out_raw, O.rmsnorm(x, out_norm, eps), 0, cfg.vocab_size, cfg.hidden_dim)
+
+
+def test_qwen2_style_biases_from_gguf(tmp_path):
+    """Q / K / V biases (Qwen2AttentionBiasTest.java, LlamaTransformerHandler.java:258-280, 758-761),
+    single-request and batched."""
+    data, layers, out_norm, out_raw, embd = model_gguf(CFG, 23, bias=True)
+    p = tmp_path / "qwen2ish.gguf"
+    p.write_bytes(data)
+    with GgufReader.open(p) as r:
+        w = D.LlamaWeights.from_gguf(r)
+    assert all(lw.bias is not None for lw in w.layers)
+    dec = D.LlamaDecoder(w, max_seq=8)
+    table = O.dequantize(O.Q6_K, embd, CFG.vocab_size, CFG.hidden_dim)
+    kc = np.zeros((CFG.num_layers, 8, CFG.kv_dim), np.float32)
+    vc = np.zeros_like(kc)
+    for pos, tok in enumerate([5, 600, 17]):
+        got = dec.forward_token(tok, pos)
+        ref = oracle_logits_bias(CFG, layers, out_norm, out_raw, table[tok], pos, kc, vc)
+        err = np.abs(got.astype(np.float64) - ref).max() / np.abs(ref).max()
+        assert err <= 1e-3, (pos, err)
+    from juno_amd.pipeline import LlamaBatchPipeline
+    pipe = LlamaBatchPipeline(w, max_seq=8, max_batch=4)
+    solo = [D.LlamaDecoder(w, max_seq=8) for _ in range(2)]
+    for pos in range(2):
+        got = pipe.forward_batch(["x", "y"], [[9 + pos], [800]], [pos, pos])
+        for dec_i, t, g in zip(solo, [9 + pos, 800], got):
+            ref = dec_i.forward_token(t, pos)
+            assert np.abs(g - ref).max() <= 1e-3 * np.abs(ref).max()
     w.close()
