@@ -16,9 +16,9 @@
 //    reference's d*sc, Q8_0 per 32-column block with d.
 //  * Activations: x is split into fp16 hi + lo limbs (x = hi + lo to ~2^-22,
 //    so only the order of summation differs from fp32) after a power-of-two
-//    scale per (column, 256-column super-block) that keeps fp16 in range.  A
-//    prep kernel writes the limbs, sub-block sums and scales once per call,
-//    super-block major, into a workspace.
+//    scale per (column, 256-column super-block) that keeps fp16 in range.
+//    Each workgroup converts the fp32 x slice of a super-block straight into
+//    its LDS image while it stages the weights (no separate prep launch).
 //  * Work split: a workgroup is kWaves waves x 32 rows, all B columns, and a
 //    range of super-blocks.  Per super-block it stages the x slice in LDS
 //    (shared by all its rows) and each wave stages its rows' packed blocks in
@@ -52,74 +52,69 @@ constexpr int kRowsPerWG = kWaves * kRowsPerWave;
 constexpr int kXPad = 8;  // halves of padding per LDS column (spreads banks)
 
 // ------------------------------------------------------------------ workspace layout
+// Split-K partials [ksplit][B][rows] f32 (only when the K range is split).
 struct XWork {
     int Bp, cols, nsb;  // padded batch, columns, super-blocks (cols / 256)
-    int rows, ksplit;  // split-K partials: [ksplit][B][rows] f32
+    int rows, ksplit;
     uint8_t *base;
-    // The prepared x is super-block major: one contiguous slab per super-block,
-    //   [hi: Bp x 256 halves][lo: Bp x 256 halves][xs: Bp x 16 halves][SI: Bp x (S, 1/scale) f32]
-    // so the slice every workgroup stages for a super-block is one linear
-    // stretch of memory (a column-major image would put the 32 column segments
-    // of a slice a power-of-two stride apart, on the same memory channels).
-    __host__ __device__ size_t slab() const { return ((size_t)Bp * 1064 + 255) & ~size_t(255); }
-    __host__ __device__ size_t x_off() const { return 0; }
-    __host__ __device__ size_t part_off() const { return x_off() + slab() * nsb; }
-    __host__ __device__ size_t bytes() const { return part_off() + (ksplit > 1 ? (size_t)ksplit * Bp * rows * 4 : 0); }  // [ksplit][B][rows]
-    __device__ float *part() const { return reinterpret_cast<float *>(base + part_off()); }
-    __device__ uint8_t *sbx(int sb) const { return base + x_off() + slab() * sb; }
-    __device__ _Float16 *hi(int sb) const { return reinterpret_cast<_Float16 *>(sbx(sb)); }
-    __device__ _Float16 *lo(int sb) const { return reinterpret_cast<_Float16 *>(sbx(sb) + (size_t)Bp * 512); }
-    __device__ _Float16 *xs(int sb) const { return reinterpret_cast<_Float16 *>(sbx(sb) + (size_t)Bp * 1024); }
-    __device__ float2 *SI(int sb) const { return reinterpret_cast<float2 *>(sbx(sb) + (size_t)Bp * 1056); }
+    __host__ __device__ size_t bytes() const { return ksplit > 1 ? (size_t)ksplit * Bp * rows * 4 : 0; }
+    __device__ float *part() const { return reinterpret_cast<float *>(base); }
 };
 
-__device__ __forceinline__ float wave_reduce_max(float v) {
+// x into the LDS image of one column and super-block, inside the GEMM: 16
+// consecutive lanes hold its 256 values, 16 each (xv).  A power-of-two scale
+// puts max |x s| in [2^12, 2^13) (exact, undone on the partial sums), then x s
+// is split into fp16 hi + lo limbs, and the 32-column sub-block sums (as hi and
+// lo halves) and the super-block sum S are formed over 4-value groups with
+// fixed butterflies (deterministic).
+__device__ __forceinline__ void stage_x_column(const float (&xv)[16], int q, _Float16 *sh_hi, _Float16 *sh_lo,
+                                               _Float16 *sh_xs, float2 *sh_S, int col, int colh) {
+    float m = 0.f;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-__device__ __forceinline__ float wave_reduce_sum(float v) {
+    for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(xv[j]));
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
-// One wave per (padded batch column, super-block): a power-of-two scale per
-// super-block puts max |x s| in [2^12, 2^13) (exact, undone on the partial
-// sums), then the hi/lo split and the sub-block and super-block sums.
-__global__ __launch_bounds__(256) void x_prep_mfma(const float *__restrict__ X, int B, XWork w) {
-    const int lane = threadIdx.x & 63;
-    const int b = blockIdx.x * 4 + (threadIdx.x >> 6), sb = blockIdx.y;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (b < B) v = *reinterpret_cast<const float4 *>(X + (size_t)b * w.cols + sb * 256 + lane * 4);
-    const float m = wave_reduce_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));  // the 16 lanes of the column
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);
     const float s = m > 0.f ? ldexpf(1.f, 13 - e) : 1.f;
-    const float e4[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
-    _Float16 *hi = w.hi(sb) + (size_t)b * 256 + lane * 4, *lo = w.lo(sb) + (size_t)b * 256 + lane * 4;
-    float sum = 0.f;
+    float g[4];  // sums of the 4-value groups
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const _Float16 h = (_Float16)e4[j];
-        const _Float16 l = (_Float16)(e4[j] - (float)h);
-        hi[j] = h;
-        lo[j] = l;
-        sum += (float)h + (float)l;
+    for (int k = 0; k < 4; k++) {
+        _Float16 h4[4], l4[4];
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float v = xv[4 * k + j] * s;
+            const _Float16 h = (_Float16)v;
+            const _Float16 l = (_Float16)(v - (float)h);
+            h4[j] = h;
+            l4[j] = l;
+            sum += (float)h + (float)l;
+        }
+        _Float16 *ph = sh_hi + col * colh + 16 * q + 4 * k, *pl = sh_lo + col * colh + 16 * q + 4 * k;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            ph[j] = h4[j];
+            pl[j] = l4[j];
+        }
+        g[k] = sum;
     }
-    // sub-block (32 columns = 8 lanes) sums, and the super-block sum
-    float sub = sum;
+    // sub-block (32 values = groups 8i .. 8i+7 = this lane and its neighbour)
+    float sub = (g[0] + g[1]) + (g[2] + g[3]);
     sub += __shfl_xor(sub, 1);
-    sub += __shfl_xor(sub, 2);
-    sub += __shfl_xor(sub, 4);
-    const float tot = wave_reduce_sum(sum);
-    _Float16 *xs = w.xs(sb) + (size_t)b * 16;
-    if ((lane & 7) == 0) {
+    if ((q & 1) == 0) {
         const _Float16 h = (_Float16)sub;
-        xs[lane >> 3] = h;
-        xs[8 + (lane >> 3)] = (_Float16)(sub - (float)h);
+        sh_xs[col * 16 + (q >> 1)] = h;
+        sh_xs[col * 16 + 8 + (q >> 1)] = (_Float16)(sub - (float)h);
     }
-    if (lane == 0) w.SI(sb)[b] = make_float2(tot, 1.f / s);
+    // super-block total: a butterfly over the column's 64 groups (across the
+    // 16 lanes, then within the lane)
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) g[k] += __shfl_xor(g[k], o);
+    const float tot = (g[0] + g[2]) + (g[1] + g[3]);
+    if (q == 0) sh_S[col] = make_float2(tot, 1.f / s);
 }
 
 // ------------------------------------------------------------------ format policies
@@ -379,14 +374,15 @@ struct FmtQ8_0 {
 // ------------------------------------------------------------------ batched kernel
 template <class F, int NT, int PD>  // NT = padded batch / 32, PD = weight prefetch depth (super-blocks)
 __global__ __launch_bounds__(kThreads) void mfma_gemm(const uint8_t *__restrict__ W, size_t pitch, int row0, int nrows,
-                                                      int nsb, int ksb, XWork xw, float *__restrict__ Y, int B) {
+                                                      int nsb, int ksb, XWork xw, const float *__restrict__ X,
+                                                      float *__restrict__ Y, int B) {
     constexpr int BP = 32 * NT;
-    constexpr int XU = BP * 32 / kThreads;  // 16-byte x units per thread per limb
+    constexpr int CPT = BP / 32;  // x columns converted per thread (16 lanes per column and super-block)
     constexpr int CH = F::kChunks;          // 16-byte chunks staged per row and super-block
     constexpr int CL = (kRowsPerWave * CH + 63) / 64;  // chunks per lane
     __shared__ __align__(16) _Float16 sh_hi[BP * COLH];
     __shared__ __align__(16) _Float16 sh_lo[BP * COLH];
-    __shared__ __align__(16) _Float16 sh_xs[F::kSums ? BP * 16 : 8];
+    __shared__ __align__(16) _Float16 sh_xs[BP * 16];
     __shared__ __align__(16) float2 sh_S[BP];  // (sum of x, 1 / column scale) per column
     __shared__ __align__(16) uint8_t sh_w[kWaves][kRowsPerWave * CH * 16];  // wave-private row blocks
 
@@ -409,8 +405,9 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm(const uint8_t *__restrict_
     const size_t myoff = row_off(c.lr);
     uint8_t *wslot = sh_w[wave];
 
-    u32x4 xh_n[XU], xl_n[XU], xs_n = {}, ch_n[PD][CL];
-    float2 S_n = make_float2(0.f, 0.f);
+    u32x4 ch_n[PD][CL];
+    float xv_n[CPT][16];  // the next super-block's raw x: column (threadIdx.x >> 4) + 32 i, values 16 q .. +16
+    const int xq = threadIdx.x & 15, xcol = threadIdx.x >> 4;
     // (a macro rather than a lambda: the register arrays must stay in VGPRs)
 #define JH_LOAD_W(ST, SB)                                                                                  \
     do {                                                                                                   \
@@ -420,14 +417,15 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm(const uint8_t *__restrict_
     } while (0)
 #define JH_LOAD_X(SB)                                                                                      \
     do {                                                                                                   \
-        const u32x4 *hp = reinterpret_cast<const u32x4 *>(xw.hi(SB));                                     \
-        const u32x4 *lp = reinterpret_cast<const u32x4 *>(xw.lo(SB));                                     \
-        _Pragma("unroll") for (int k = 0; k < XU; k++) {                                                   \
-            xh_n[k] = hp[threadIdx.x + kThreads * k];                                                      \
-            xl_n[k] = lp[threadIdx.x + kThreads * k];                                                      \
+        _Pragma("unroll") for (int i = 0; i < CPT; i++) {                                                  \
+            const int b = xcol + 32 * i;                                                                   \
+            const float4 *xp = reinterpret_cast<const float4 *>(X + (size_t)min(b, B - 1) * xw.cols +     \
+                                                                (SB) * 256 + 16 * xq);                     \
+            _Pragma("unroll") for (int k = 0; k < 4; k++) {                                                \
+                const float4 v = b < B ? xp[k] : make_float4(0.f, 0.f, 0.f, 0.f);                         \
+                xv_n[i][4 * k] = v.x; xv_n[i][4 * k + 1] = v.y; xv_n[i][4 * k + 2] = v.z; xv_n[i][4 * k + 3] = v.w; \
+            }                                                                                              \
         }                                                                                                  \
-        if (F::kSums) xs_n = reinterpret_cast<const u32x4 *>(xw.xs(SB))[min((int)threadIdx.x, BP * 2 - 1)]; \
-        S_n = xw.SI(SB)[min((int)threadIdx.x, BP - 1)];                                                    \
     } while (0)
 
     f32x16 tot[NT];
@@ -441,14 +439,8 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm(const uint8_t *__restrict_
     for (int sb = sb0; sb < sb1; sb++) {
         __syncthreads();  // the previous super-block's LDS contents are consumed
 #pragma unroll
-        for (int k = 0; k < XU; k++) {
-            const int i = threadIdx.x + kThreads * k, col = i >> 5, u = i & 31;
-            *reinterpret_cast<u32x4 *>(sh_hi + col * COLH + 8 * u) = xh_n[k];
-            *reinterpret_cast<u32x4 *>(sh_lo + col * COLH + 8 * u) = xl_n[k];
-        }
-        if (F::kSums && threadIdx.x < BP * 2)
-            *reinterpret_cast<u32x4 *>(sh_xs + (threadIdx.x >> 1) * 16 + 8 * (threadIdx.x & 1)) = xs_n;
-        if (threadIdx.x < BP) sh_S[threadIdx.x] = S_n;
+        for (int i = 0; i < CPT; i++)
+            stage_x_column(xv_n[i], xq, sh_hi, sh_lo, sh_xs, sh_S, xcol + 32 * i, COLH);
 #pragma unroll
         for (int k = 0; k < CL; k++)
             if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot + 16 * (lane + 64 * k)) = ch_n[0][k];
@@ -544,7 +536,7 @@ size_t mfma_workspace_bytes(int type, int B, int cols, int rows) {
     int tiles, ksplit, ksb;
     mfma_split(rows, cols / 256, tiles, ksplit, ksb);
     XWork w{(B + 31) / 32 * 32, cols, cols / 256, rows, ksplit, nullptr};
-    return w.bytes();
+    return w.bytes() > 256 ? w.bytes() : 256;  // nonzero: the MFMA path applies
 }
 
 hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s) {
@@ -558,11 +550,8 @@ hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s
     int tiles, ksplit, ksb;
     mfma_split(nrows, nsb, tiles, ksplit, ksb);
     XWork w{Bp, a.cols, nsb, nrows, ksplit, reinterpret_cast<uint8_t *>(workspace)};
-    x_prep_mfma<<<dim3(Bp / 4, nsb), 256, 0, s>>>(a.x, B, w);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
     dim3 grid(tiles, ksplit);
-#define JH_GEMM(F, NT) mfma_gemm<F, NT, NT == 1 ? kPrefetch : 1><<<grid, kThreads, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.y, B)
+#define JH_GEMM(F, NT) mfma_gemm<F, NT, NT == 1 ? kPrefetch : 1><<<grid, kThreads, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.x, a.y, B)
     if (a.type == 12) {
         if (Bp == 32) JH_GEMM(FmtQ4K, 1); else JH_GEMM(FmtQ4K, 2);
     } else if (a.type == 13) {
@@ -573,7 +562,7 @@ hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s
         if (Bp == 32) JH_GEMM(FmtQ8_0, 1); else JH_GEMM(FmtQ8_0, 2);
     }
 #undef JH_GEMM
-    e = hipGetLastError();
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess || ksplit == 1) return e;
     const int n = B * nrows;
     if (n % 4 == 0 && reinterpret_cast<uintptr_t>(a.y) % 16 == 0)
