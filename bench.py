@@ -88,7 +88,8 @@ def make_step(torch, L, mats, B, stream, grouped=True):
     launch for [q, k, v] (same input), [o], one for [gate, up] (same input),
     [down]; then the lm_head.  Each stage has its own input vector, as in a
     real step (attention-norm output, attention output, FFN-norm output,
-    SwiGLU product).  B > 1 calls the batched entry point per matrix."""
+    SwiGLU product).  B > 1 groups the same way through the batched group
+    entry point (one MFMA launch per group at B >= 16)."""
     g = torch.Generator(device="cuda")
     g.manual_seed(1)
     x_attn = torch.randn(B, HIDDEN, generator=g, device="cuda")
@@ -105,7 +106,7 @@ def make_step(torch, L, mats, B, stream, grouped=True):
         for names in (["attn_q", "attn_k", "attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"], ["ffn_down"]):
             stages.append([f"blk.{layer}.{n}" for n in names])
     stages.append(["output"])
-    if not grouped or B != 1:
+    if not grouped:
         stages = [[m[0]] for m in mats]
 
     def xin(name):
@@ -125,11 +126,10 @@ def make_step(torch, L, mats, B, stream, grouped=True):
         assert keep
         s = ctypes.c_void_p(stream.cuda_stream)
         for st, n, hs, xp, yp in packed:
-            if B == 1 and grouped:
+            if B == 1:
                 rc = L.jh_qmatvec_group_dev(n, hs, xp, yp, s)
             else:
-                _, rows, cols, _, dev = by_name[st[0]]
-                rc = L.jh_qmatvec_batched_dev(dev.handle, xp[0], B, yp[0], 0, rows, s)
+                rc = L.jh_qmatvec_batched_group_dev(n, hs, xp, B, yp, s)
             if rc:
                 raise RuntimeError(L.jh_last_error().decode())
     return launch, len(packed)

@@ -148,6 +148,16 @@ int jh_qmat_dequant_dev(const jh_qmat *m, float *d_out, void *stream);
 int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *d_x, float *const *d_y,
                          void *stream);
 
+/* Batched form of jh_qmatvec_group_dev: Y_i[B][rows_i] = X_i[B][cols] W_i^T
+ * for n <= 4 matrices, full row ranges, one launch when B >= 16 and the
+ * matrices share cols (the MFMA path; formats may differ, e.g. the Q4_K q / k
+ * and Q6_K v of a Q4_K_M layer), else one call per matrix.  Same results as
+ * n calls of jh_qmatvec_batched_dev.  The reference's forwardBatch runs the
+ * requests one by one (InferencePipeline.java:62-69); this is the grouped
+ * projection step of its batched replacement. */
+int jh_qmatvec_batched_group_dev(int n, const jh_qmat *const *mats, const float *const *d_X, int B,
+                                 float *const *d_Y, void *stream);
+
 /* Raw-pointer variant of the quantizer: n fp32 values -> packed bytes in a
  * caller-provided device buffer of rawByteCount(type, n) bytes. */
 int jh_quantize_dev(int ggml_type, const float *d_src, int64_t n, void *d_dst, void *stream);

@@ -188,6 +188,30 @@ int gemv_path();
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> g_ws;
 
+// Split-K tile counters of the batched MFMA path, one 4 KB block per
+// (device, stream), zeroed when allocated (so the first use must be eager,
+// like the workspace's); every launch leaves them zero again.
+std::map<std::pair<int, hipStream_t>, int *> g_counters;
+
+int stream_counters(int device, hipStream_t s, int **out) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    int *&c = g_counters[{device, s}];
+    if (!c) {
+        void *p = nullptr;
+        int rc = device_alloc(&p, 4096);
+        if (rc) return rc;
+        hipError_t e = hipMemset(p, 0, 4096);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return hip_fail("counter init", e);
+        }
+        c = static_cast<int *>(p);
+    }
+    *out = c;
+    return JH_OK;
+}
+
 int stream_workspace(int device, hipStream_t s, size_t bytes, void **out) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     auto &e = g_ws[{device, s}];
@@ -206,6 +230,25 @@ int stream_workspace(int device, hipStream_t s, size_t bytes, void **out) {
     return JH_OK;
 }
 
+// The MFMA path for a group of matrices sharing K (B >= 16): kMfmaNotApplicable
+// (never returned through the C ABI) when it does not apply, so that the caller
+// can take the per-matrix kernels.
+constexpr int kMfmaNotApplicable = -1;
+
+int enqueue_mfma_group(int device, int n, const jh::MfmaDesc *d, int B, hipStream_t s) {
+    const size_t wsb = jh::mfma_group_workspace_bytes(n, d, B);
+    if (!wsb) return kMfmaNotApplicable;
+    void *ws = nullptr;
+    int *counters = nullptr;
+    int rc = stream_workspace(device, s, wsb, &ws);
+    if (!rc) rc = stream_counters(device, s, &counters);
+    if (rc) return rc;
+    hipError_t e = jh::launch_mfma_group(n, d, B, ws, counters, s);
+    if (e == hipSuccess) return JH_OK;
+    if (e == hipErrorNotSupported) return kMfmaNotApplicable;
+    return hip_fail("mfma_group launch", e);
+}
+
 // Enqueue y = W x for B vectors (device pointers), splitting B into the
 // kernel's supported batch widths, or using the MFMA path for B >= 16.
 int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int row_start, int row_end,
@@ -222,18 +265,9 @@ int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int ro
     a.ldx = m->cols;
     a.ldy = nrows;
     if (B >= 16) {
-        const size_t wsb = jh::mfma_workspace_bytes(m->type, B, m->cols, row_end - row_start);
-        if (wsb) {
-            void *ws = nullptr;
-            int rc = stream_workspace(m->ctx->device, s, wsb, &ws);
-            if (rc) return rc;
-            a.batch = B;
-            a.x = d_x;
-            a.y = d_y;
-            hipError_t e = jh::launch_gemm_mfma_ws(a, ws, s);
-            if (e == hipSuccess) return JH_OK;
-            if (e != hipErrorNotSupported) return hip_fail("gemm_mfma launch", e);
-        }
+        const jh::MfmaDesc d{m->type, m->d_raw, m->pitch, m->cols, row_start, row_end, d_x, d_y};
+        int rc = enqueue_mfma_group(m->ctx->device, 1, &d, B, s);
+        if (rc != kMfmaNotApplicable) return rc;
     }
     if (B == 1 && gemv_path() != 1) {
         a.batch = 1;
@@ -562,6 +596,30 @@ int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *
         hipError_t e = jh::launch_gemv_group(g, s);
         if (e != hipSuccess) return hip_fail("gemv_group launch", e);
     }
+    return ok();
+}
+
+int jh_qmatvec_batched_group_dev(int n, const jh_qmat *const *mats, const float *const *d_X, int B,
+                                 float *const *d_Y, void *stream) {
+    if (n < 0 || n > jh::kMaxMfmaGroup) return fail(JH_EINVAL, "n=%d outside [0, %d]", n, jh::kMaxMfmaGroup);
+    if (B < 0) return fail(JH_EINVAL, "B=%d must be >= 0", B);
+    if (n == 0 || B == 0) return ok();
+    if (!mats || !d_X || !d_Y) return fail(JH_EINVAL, "mats, X and Y must not be null");
+    int rc;
+    jh::MfmaDesc d[jh::kMaxMfmaGroup];
+    for (int i = 0; i < n; i++) {
+        if ((rc = check_qmat(mats[i]))) return rc;
+        if (!d_X[i] || !d_Y[i]) return fail(JH_EINVAL, "X[%d] and Y[%d] must not be null", i, i);
+        if (mats[i]->ctx->device != mats[0]->ctx->device) return fail(JH_EINVAL, "matrices on different devices");
+        d[i] = jh::MfmaDesc{mats[i]->type, mats[i]->d_raw, mats[i]->pitch, mats[i]->cols, 0, mats[i]->rows, d_X[i], d_Y[i]};
+    }
+    hipStream_t s = (hipStream_t)stream;
+    if (B >= 16) {
+        rc = enqueue_mfma_group(mats[0]->ctx->device, n, d, B, s);
+        if (rc != kMfmaNotApplicable) return rc ? rc : ok();
+    }
+    for (int i = 0; i < n; i++)
+        if ((rc = enqueue_matvec(mats[i], d_X[i], B, d_Y[i], 0, mats[i]->rows, s))) return rc;
     return ok();
 }
 

@@ -56,12 +56,24 @@ bool staged_supported(int type, int cols);
 hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s);
 
 // Batched decode through the LDS-staged, fp16-MFMA path (16 <= B <= 64).
-// mfma_workspace_bytes returns 0 when the path does not apply (type / shape);
-// otherwise launch_gemm_mfma_ws needs that many bytes of device workspace,
-// which must not be in use by another stream while the launch runs (its
-// contents need not be initialised).
-size_t mfma_workspace_bytes(int type, int B, int cols, int rows);
-hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s);
+// Batched GEMVs (16 <= B <= 64) on fp16 MFMA: up to kMaxMfmaGroup matrices
+// with the same cols, each with its own x [B][cols] and y [B][row_end -
+// row_start], in one launch.  mfma_group_workspace_bytes returns 0 when the
+// path does not apply (types, shapes, alignment); otherwise launch_mfma_group
+// needs that many bytes of device workspace and 1024 ints of counters that
+// are zero before the first launch and that every launch leaves zero (the
+// split-K hand-off counts a tile's splits there).
+struct MfmaDesc {
+    int type;
+    const uint8_t *w;
+    size_t pitch;
+    int cols, row_start, row_end;
+    const float *x;
+    float *y;
+};
+constexpr int kMaxMfmaGroup = 4;
+size_t mfma_group_workspace_bytes(int n, const MfmaDesc *d, int B);
+hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, int *counters, hipStream_t s);
 
 // out[rows][cols] fp32, bit-exact with the reference dequantizers.
 hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float *out, hipStream_t s);

@@ -51,16 +51,6 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kRowsPerWG = kWaves * kRowsPerWave;
 constexpr int kXPad = 8;  // halves of padding per LDS column (spreads banks)
 
-// ------------------------------------------------------------------ workspace layout
-// Split-K partials [ksplit][B][rows] f32 (only when the K range is split).
-struct XWork {
-    int Bp, cols, nsb;  // padded batch, columns, super-blocks (cols / 256)
-    int rows, ksplit;
-    uint8_t *base;
-    __host__ __device__ size_t bytes() const { return ksplit > 1 ? (size_t)ksplit * Bp * rows * 4 : 0; }
-    __device__ float *part() const { return reinterpret_cast<float *>(base); }
-};
-
 // x into the LDS image of one column and super-block, inside the GEMM: 16
 // consecutive lanes hold its 256 values, 16 each (xv).  A power-of-two scale
 // puts max |x s| in [2^12, 2^13) (exact, undone on the partial sums), then x s
@@ -127,12 +117,51 @@ __device__ __forceinline__ void stage_x_column(const float (&xv)[16], int q, _Fl
 // enters the MFMA as an exact fp16 integer; scales are applied in fp32.
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
+constexpr int COLH = 256 + kXPad;  // halves per LDS column of the staged x slice
+
+// x fragments of the padded image the fused kernel converts into LDS: column
+// col at col * COLH halves (hi and lo), its sub-block sums at col * 16.
 struct Ctx {
     int wave, lr, kh;
     const _Float16 *sh_hi, *sh_lo, *sh_xs;
     const float2 *sh_S;
+    __device__ __forceinline__ half8 xh(int col, int xoff) const {
+        return *reinterpret_cast<const half8 *>(sh_hi + col * COLH + xoff);
+    }
+    __device__ __forceinline__ half8 xl(int col, int xoff) const {
+        return *reinterpret_cast<const half8 *>(sh_lo + col * COLH + xoff);
+    }
+    __device__ __forceinline__ half8 xm(int col) const { return *reinterpret_cast<const half8 *>(sh_xs + col * 16 + 8 * kh); }
+    __device__ __forceinline__ const float2 *S() const { return sh_S; }
 };
-constexpr int COLH = 256 + kXPad;  // halves per LDS column of the staged x slice
+
+// ------------------------------------------------------------------ prepared x (B <= 32)
+// One super-block of x for 32 batch columns, laid out exactly as the GEMM's
+// LDS image so that it moves in as a contiguous DMA copy:
+//   [hi: 32 columns x 32 units][lo: the same][sub-block sums: 32 x 16 halves]
+//   [(S, 1 / scale): 32 x float2][pad to 34 x 1 KB]
+// A unit is 16 bytes (8 consecutive values of one column).  Unit u of column
+// col sits at slot col * 32 + (u ^ (col & 31)): the XOR swizzle lets the 32
+// lanes that read unit u of 32 columns hit distinct LDS banks without padding.
+constexpr int kSlabHi = 0, kSlabLo = 16384, kSlabXs = 32768, kSlabS = 33792;
+constexpr int kSlabRows = 34;  // 1 KB DMA rows
+constexpr int kSlabBytes = kSlabRows * 1024;
+
+struct CtxP {
+    int lr, kh;
+    const uint8_t *x;  // the slab in LDS
+    __device__ __forceinline__ static int slot(int col, int xoff) { return (col << 5) | ((xoff >> 3) ^ (col & 31)); }
+    __device__ __forceinline__ half8 xh(int col, int xoff) const {
+        return *reinterpret_cast<const half8 *>(x + kSlabHi + 16 * slot(col, xoff));
+    }
+    __device__ __forceinline__ half8 xl(int col, int xoff) const {
+        return *reinterpret_cast<const half8 *>(x + kSlabLo + 16 * slot(col, xoff));
+    }
+    __device__ __forceinline__ half8 xm(int col) const {
+        return *reinterpret_cast<const half8 *>(x + kSlabXs + 32 * col + 16 * kh);
+    }
+    __device__ __forceinline__ const float2 *S() const { return reinterpret_cast<const float2 *>(x + kSlabS); }
+};
 
 // Operand roles: x is the A operand (its 32 rows are batch columns) and the
 // weights are B, so D[b][r] = sum_k x[b][k] w[r][k].  In the 32x32x16 layout
@@ -157,26 +186,26 @@ __device__ __forceinline__ half8 bytes_to_h8(uint32_t w0, uint32_t w1, half2v of
 }
 
 // acc[n] += x_hi . w + x_lo . w over one K-step (x columns at xoff)
-template <int NT>
-__device__ __forceinline__ void mfma_xw(const Ctx &c, const half8 &w, int xoff, f32x16 *acc) {
+template <int NT, class C>
+__device__ __forceinline__ void mfma_xw(const C &c, const half8 &w, int xoff, f32x16 *acc) {
 #pragma unroll
     for (int n = 0; n < NT; n++) {
         const int col = n * 32 + c.lr;
-        const half8 xh = *reinterpret_cast<const half8 *>(c.sh_hi + col * COLH + xoff);
-        const half8 xl = *reinterpret_cast<const half8 *>(c.sh_lo + col * COLH + xoff);
+        const half8 xh = c.xh(col, xoff);
+        const half8 xl = c.xl(col, xoff);
         acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xh, w, acc[n], 0, 0, 0);
         acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xl, w, acc[n], 0, 0, 0);
     }
 }
 
 // (S, 1/scale) of the 16 batch columns a lane holds for tile n
-template <int NT>
-__device__ __forceinline__ void col_terms(const Ctx &c, int n, float (&S)[16], float (&cs)[16]) {
+template <int NT, class C>
+__device__ __forceinline__ void col_terms(const C &c, int n, float (&S)[16], float (&cs)[16]) {
 #pragma unroll
     for (int q = 0; q < 4; q++)
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const float4 v = *reinterpret_cast<const float4 *>(c.sh_S + n * 32 + 8 * q + 4 * c.kh + 2 * h);
+            const float4 v = *reinterpret_cast<const float4 *>(c.S() + n * 32 + 8 * q + 4 * c.kh + 2 * h);
             S[4 * q + 2 * h] = v.x;
             cs[4 * q + 2 * h] = v.y;
             S[4 * q + 2 * h + 1] = v.z;
@@ -214,8 +243,8 @@ struct FmtKQ {
             r.qh[1] = *reinterpret_cast<const u32x2 *>(p + 32 + 8 * kh);
         }
     }
-    template <int NT>
-    static __device__ __forceinline__ void compute(const Regs &r, const Ctx &c, f32x16 *tot) {
+    template <int NT, class C>
+    static __device__ __forceinline__ void compute(const Regs &r, const C &c, f32x16 *tot) {
         // 6-bit scales and mins of the 8 sub-blocks (q4kScaleRaw / q4kMinRaw, :1471-1482)
         int ls[8], lm[8];
 #pragma unroll
@@ -266,7 +295,7 @@ struct FmtKQ {
 #pragma unroll
         for (int n = 0; n < NT; n++) {
             const int col = n * 32 + c.lr;
-            const half8 xm = *reinterpret_cast<const half8 *>(c.sh_xs + col * 16 + 8 * c.kh);
+            const half8 xm = c.xm(col);
             const f32x16 mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(xm, wm, (f32x16){}, 0, 0, 0);
             float S[16], cs[16];
             col_terms<NT>(c, n, S, cs);
@@ -307,8 +336,8 @@ struct FmtQ6K {
         r.sc = *reinterpret_cast<const u32x4a2 *>(p + 192);
         r.dw = *reinterpret_cast<const u32a2 *>(p + 206);
     }
-    template <int NT>
-    static __device__ __forceinline__ void compute(const Regs &r, const Ctx &c, f32x16 *tot) {
+    template <int NT, class C>
+    static __device__ __forceinline__ void compute(const Regs &r, const C &c, f32x16 *tot) {
         const half2v off = {(_Float16)1056.f, (_Float16)1056.f};  // 1024 + 32
         const float d = half_bits_to_float(r.dw >> 16);
 #pragma unroll
@@ -348,8 +377,8 @@ struct FmtQ8_0 {
             r.d[b] = *reinterpret_cast<const uint16_t *>(p + 34 * b);
         }
     }
-    template <int NT>
-    static __device__ __forceinline__ void compute(const Regs &r, const Ctx &c, f32x16 *tot) {
+    template <int NT, class C>
+    static __device__ __forceinline__ void compute(const Regs &r, const C &c, f32x16 *tot) {
         const half2v off = {(_Float16)1152.f, (_Float16)1152.f};  // 1024 + 128
 #pragma unroll
         for (int b = 0; b < 8; b++) {
@@ -371,26 +400,152 @@ struct FmtQ8_0 {
     }
 };
 
+// ------------------------------------------------------------------ tile output
+// A workgroup's tile goes straight into y when K is not split.  Otherwise
+// each split stores its partial tile with coherent (L2-bypassing) stores and
+// bumps the tile's counter; the split that arrives last adds all partials in
+// split order into y -- a fixed order, whatever the arrival order, so the
+// result is deterministic -- and re-arms the counter for the next launch.
+// Coherent stores plus a wait for their completion before the counter
+// increment avoid a device-scope release, which on a multi-XCD part writes
+// back the whole L2 (~100 us per workgroup measured); a separate reduction
+// launch costs ~5 us.
+constexpr int kMaxTileCounters = 1024;
+
+template <int NT>
+__device__ __forceinline__ void store_tile(const f32x16 (&tot)[NT], int r, int nrows, int kh, int B, float *__restrict__ Y,
+                                           float *part, int *counters, int tile, int split, int ksplit) {
+    const bool live = r < nrows;
+    if (ksplit == 1) {
+        if (!live) return;
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int b = batch_of(n, i, kh);
+                if (b < B) Y[(size_t)b * nrows + r] = tot[n][i];
+            }
+        return;
+    }
+    const size_t plane = (size_t)B * nrows;
+    if (live) {
+        float *mine = part + split * plane;
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int b = batch_of(n, i, kh);
+                if (b < B) __hip_atomic_store(mine + (size_t)b * nrows + r, tot[n][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have reached the coherence point
+    __shared__ int s_last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == ksplit - 1;
+        if (last) __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last || !live) return;
+    // KB splits' partials in flight at a time, added in split order
+    constexpr int KB = 4 / NT;
+    const int ks = ksplit;
+    float acc[NT][16];
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[n][i] = 0.f;
+    for (int k0 = 0; k0 < ks; k0 += KB) {
+        float v[KB][NT][16];
+#pragma unroll
+        for (int kk = 0; kk < KB; kk++) {
+            const int k = k0 + kk;
+#pragma unroll
+            for (int n = 0; n < NT; n++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    // unconditional (clamped) loads, so that they issue back to back;
+                    // this split's own partial comes back from memory unchanged
+                    const int b = min(batch_of(n, i, kh), B - 1);
+                    v[kk][n][i] = __hip_atomic_load(part + min(k, ks - 1) * plane + (size_t)b * nrows + r,
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+        }
+#pragma unroll
+        for (int kk = 0; kk < KB; kk++)
+            if (k0 + kk < ks)
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) acc[n][i] += v[kk][n][i];
+    }
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int b = batch_of(n, i, kh);
+            if (b < B) Y[(size_t)b * nrows + r] = acc[n][i];
+        }
+}
+
 // ------------------------------------------------------------------ batched kernel
+// One matrix of a grouped launch: the workgroups [wg0, wg0 + tiles * ksplit)
+// are its row tiles x K splits (split fastest); its partial planes start at
+// part0 floats into the group's partial buffer and its tile counters at cnt0.
+struct MfmaProblem {
+    const uint8_t *w;
+    const float *x;
+    float *y;
+    size_t pitch, part0;
+    int type, row0, rows, tiles, wg0, cnt0;
+};
+struct MfmaGroup {
+    MfmaProblem p[kMaxMfmaGroup];
+    float *part;
+    int *counters;
+    int n, nsb, ksb, ksplit, B;
+};
+
+// format mask bits: Q4_K, Q5_K, Q6_K, Q8_0
+template <int MASK>
+__host__ __device__ constexpr int max_chunks() {
+    int c = 0;
+    if (MASK & 1) c = c > FmtQ4K::kChunks ? c : FmtQ4K::kChunks;
+    if (MASK & 2) c = c > FmtQ5K::kChunks ? c : FmtQ5K::kChunks;
+    if (MASK & 4) c = c > FmtQ6K::kChunks ? c : FmtQ6K::kChunks;
+    if (MASK & 8) c = c > FmtQ8_0::kChunks ? c : FmtQ8_0::kChunks;
+    return c;
+}
+// LDS image: [x hi: BP x COLH][x lo: BP x COLH][sums: BP x 16 halves][(S, 1/s): BP][weight windows]
+template <int NT>
+__host__ __device__ constexpr int lds_w_offset() { return (2 * 32 * NT * COLH + 32 * NT * 16) * 2 + 32 * NT * 8; }
+template <int NT, int MASK>
+__host__ __device__ constexpr int lds_bytes() { return lds_w_offset<NT>() + kWaves * kRowsPerWave * max_chunks<MASK>() * 16; }
+
+// One workgroup's tile (32 rows per wave x all batch columns) over the K
+// range of its split, x converted into LDS super-block by super-block.
 template <class F, int NT, int PD>  // NT = padded batch / 32, PD = weight prefetch depth (super-blocks)
-__global__ __launch_bounds__(kThreads) void mfma_gemm(const uint8_t *__restrict__ W, size_t pitch, int row0, int nrows,
-                                                      int nsb, int ksb, XWork xw, const float *__restrict__ X,
-                                                      float *__restrict__ Y, int B) {
+__device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int split, const MfmaGroup &g, uint8_t *lds) {
     constexpr int BP = 32 * NT;
     constexpr int CPT = BP / 32;  // x columns converted per thread (16 lanes per column and super-block)
     constexpr int CH = F::kChunks;          // 16-byte chunks staged per row and super-block
     constexpr int CL = (kRowsPerWave * CH + 63) / 64;  // chunks per lane
-    __shared__ __align__(16) _Float16 sh_hi[BP * COLH];
-    __shared__ __align__(16) _Float16 sh_lo[BP * COLH];
-    __shared__ __align__(16) _Float16 sh_xs[BP * 16];
-    __shared__ __align__(16) float2 sh_S[BP];  // (sum of x, 1 / column scale) per column
-    __shared__ __align__(16) uint8_t sh_w[kWaves][kRowsPerWave * CH * 16];  // wave-private row blocks
+    _Float16 *sh_hi = reinterpret_cast<_Float16 *>(lds);
+    _Float16 *sh_lo = sh_hi + BP * COLH;
+    _Float16 *sh_xs = sh_lo + BP * COLH;
+    float2 *sh_S = reinterpret_cast<float2 *>(sh_xs + BP * 16);  // (sum of x, 1 / column scale) per column
+    const uint8_t *__restrict__ W = P.w;
+    const float *__restrict__ X = P.x;
+    const size_t pitch = P.pitch;
+    const int nrows = P.rows, row0 = P.row0, B = g.B, cols = 256 * g.nsb;
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const Ctx c{wave, lane & 31, lane >> 5, sh_hi, sh_lo, sh_xs, sh_S};
-    const int rbase = blockIdx.x * kRowsPerWG + wave * kRowsPerWave;
-    const int sb0 = blockIdx.y * ksb, sb1 = min(nsb, sb0 + ksb);
+    const int rbase = tile * kRowsPerWG + wave * kRowsPerWave;
+    const int sb0 = split * g.ksb, sb1 = min(g.nsb, sb0 + g.ksb);
     auto row_off = [&](int rho) { return (size_t)(row0 + min(rbase + rho, nrows - 1)) * pitch; };
     // Weight staging: chunk j = lane + 64 k of the wave's 32 x CH chunk grid is
     // row j / CH, 16-byte piece j % CH of that row's aligned window.  Whole
@@ -403,7 +558,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm(const uint8_t *__restrict_
         coff[k] = row_off(j / CH) + 16 * (j % CH);
     }
     const size_t myoff = row_off(c.lr);
-    uint8_t *wslot = sh_w[wave];
+    uint8_t *wslot = lds + lds_w_offset<NT>() + wave * (kRowsPerWave * CH * 16);
 
     u32x4 ch_n[PD][CL];
     float xv_n[CPT][16];  // the next super-block's raw x: column (threadIdx.x >> 4) + 32 i, values 16 q .. +16
@@ -419,7 +574,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm(const uint8_t *__restrict_
     do {                                                                                                   \
         _Pragma("unroll") for (int i = 0; i < CPT; i++) {                                                  \
             const int b = xcol + 32 * i;                                                                   \
-            const float4 *xp = reinterpret_cast<const float4 *>(X + (size_t)min(b, B - 1) * xw.cols +     \
+            const float4 *xp = reinterpret_cast<const float4 *>(X + (size_t)min(b, B - 1) * cols +        \
                                                                 (SB) * 256 + 16 * xq);                     \
             _Pragma("unroll") for (int k = 0; k < 4; k++) {                                                \
                 const float4 v = b < B ? xp[k] : make_float4(0.f, 0.f, 0.f, 0.f);                         \
@@ -474,101 +629,312 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm(const uint8_t *__restrict_
 #undef JH_LOAD_X
 #undef JH_LOAD_W
 
-    // a single split writes y; otherwise each split writes its partial tile
-    // and reduce_splits adds them in split order (deterministic).  A hand-off
-    // between workgroups inside this kernel would need a device-scope release
-    // per workgroup, which on a multi-XCD part writes back the whole L2 each
-    // time (~100 us measured).
-    const int r = rbase + c.lr;
-    if (r >= nrows) return;
-    float *out = gridDim.y == 1 ? Y : xw.part() + (size_t)blockIdx.y * B * nrows;
-#pragma unroll
-    for (int n = 0; n < NT; n++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int b = batch_of(n, i, c.kh);
-            if (b < B) out[(size_t)b * nrows + r] = tot[n][i];
-        }
+    store_tile<NT>(tot, rbase + c.lr, nrows, c.kh, B, P.y, g.part + P.part0, g.counters + P.cnt0, tile, split,
+                   g.ksplit);
 }
 
-// y[i] = sum over splits k (in order) of part[k][i]; V outputs per thread
-template <typename T>
-__device__ __forceinline__ void add_to(T &a, const T &b) { a += b; }
-template <>
-__device__ __forceinline__ void add_to<float4>(float4 &a, const float4 &b) {
-    a.x += b.x;
-    a.y += b.y;
-    a.z += b.z;
-    a.w += b.w;
-}
-template <typename T>
-__global__ __launch_bounds__(256) void reduce_splits(XWork xw, int n, int ksplit, float *__restrict__ Y) {
-    const T *p = reinterpret_cast<const T *>(xw.part());
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
-        T v[16];
-        T acc{};
-        for (int k0 = 0; k0 < ksplit; k0 += 16) {
-            const int nk = min(16, ksplit - k0);
-#pragma unroll
-            for (int k = 0; k < 16; k++)
-                if (k < nk) v[k] = p[(size_t)(k0 + k) * n + i];
-#pragma unroll
-            for (int k = 0; k < 16; k++)
-                if (k < nk) add_to(acc, v[k]);
-        }
-        reinterpret_cast<T *>(Y)[i] = acc;
+// A group of matrices with the same K in one launch (1-D grid): each
+// workgroup finds its matrix and runs that matrix's format.
+template <int NT, int MASK>
+__global__ __launch_bounds__(kThreads) void mfma_group(MfmaGroup g) {
+    __shared__ __align__(16) uint8_t lds[lds_bytes<NT, MASK>()];
+    const int id = blockIdx.x;
+    int m = 0;
+    for (int i = 1; i < g.n; i++)
+        if (id >= g.p[i].wg0) m = i;
+    const MfmaProblem &P = g.p[m];
+    const int local = id - P.wg0, tile = local / g.ksplit, split = local - tile * g.ksplit;
+    constexpr int PD = NT == 1 ? kPrefetch : 1;
+    switch (P.type) {
+        case 12: if constexpr ((MASK & 1) != 0) gemm_body<FmtQ4K, NT, PD>(P, tile, split, g, lds); break;
+        case 13: if constexpr ((MASK & 2) != 0) gemm_body<FmtQ5K, NT, PD>(P, tile, split, g, lds); break;
+        case 14: if constexpr ((MASK & 4) != 0) gemm_body<FmtQ6K, NT, PD>(P, tile, split, g, lds); break;
+        default: if constexpr ((MASK & 8) != 0) gemm_body<FmtQ8_0, NT, PD>(P, tile, split, g, lds); break;
     }
+}
+
+// x of one column and super-block into its prepared slab: 16 consecutive
+// lanes hold the column's 256 values, 16 each (xv).  The same arithmetic as
+// stage_x_column (scale, limbs, sums, butterflies), so both layouts carry
+// identical values.
+__device__ __forceinline__ void prep_x_column(const float (&xv)[16], int q, uint8_t *slab, int col) {
+    float m = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(xv[j]));
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    int e = 0;
+    if (m > 0.f) (void)frexpf(m, &e);
+    const float s = m > 0.f ? ldexpf(1.f, 13 - e) : 1.f;
+    half8 h[2], l[2];
+    float g[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float v = xv[4 * k + j] * s;
+            const _Float16 hh = (_Float16)v;
+            const _Float16 ll = (_Float16)(v - (float)hh);
+            h[k >> 1][4 * (k & 1) + j] = hh;
+            l[k >> 1][4 * (k & 1) + j] = ll;
+            sum += (float)hh + (float)ll;
+        }
+        g[k] = sum;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int slot = CtxP::slot(col, 8 * (2 * q + i));
+        *reinterpret_cast<half8 *>(slab + kSlabHi + 16 * slot) = h[i];
+        *reinterpret_cast<half8 *>(slab + kSlabLo + 16 * slot) = l[i];
+    }
+    float sub = (g[0] + g[1]) + (g[2] + g[3]);
+    sub += __shfl_xor(sub, 1);
+    if ((q & 1) == 0) {
+        _Float16 *xs = reinterpret_cast<_Float16 *>(slab + kSlabXs) + col * 16;
+        const _Float16 hs = (_Float16)sub;
+        xs[q >> 1] = hs;
+        xs[8 + (q >> 1)] = (_Float16)(sub - (float)hs);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) g[k] += __shfl_xor(g[k], o);
+    const float tot = (g[0] + g[2]) + (g[1] + g[3]);
+    if (q == 0) reinterpret_cast<float2 *>(slab + kSlabS)[col] = make_float2(tot, 1.f / s);
+}
+
+// one workgroup per super-block: 32 columns x 16 lanes (columns >= B are zero)
+__global__ __launch_bounds__(512) void x_prep(const float *__restrict__ X, int B, int cols, uint8_t *__restrict__ slabs) {
+    const int sb = blockIdx.x, q = threadIdx.x & 15, col = threadIdx.x >> 4;
+    float xv[16];
+    const float4 *xp = reinterpret_cast<const float4 *>(X + (size_t)min(col, B - 1) * cols + sb * 256 + 16 * q);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float4 v = col < B ? xp[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+        xv[4 * k] = v.x;
+        xv[4 * k + 1] = v.y;
+        xv[4 * k + 2] = v.z;
+        xv[4 * k + 3] = v.w;
+    }
+    prep_x_column(xv, q, slabs + (size_t)sb * kSlabBytes, col);
+}
+
+// The B <= 32 kernel on prepared x, for matrices with enough row tiles to
+// fill the GPU without splitting K (the output projection).  It reads x once
+// per super-block from a slab that x_prep wrote, instead of converting it in
+// every workgroup.  Per super-block each wave:
+//  1. waits until its share of this super-block's x slab (DMA) and its
+//     weight chunks have landed, and meets the others at the one barrier;
+//  2. starts the DMA of the next slab into the other LDS buffer (everyone has
+//     finished the super-block that used it);
+//  3. moves its weight chunks through its LDS window into the format's
+//     registers and starts the loads of the super-block after next into the
+//     freed register set (two sets alternate: weights stay two super-blocks
+//     ahead with no register copies);
+//  4. runs the MFMAs.
+// Loads are issued unconditionally (addresses clamped to the last super-block
+// of the range) so that every wave's count of memory operations in flight is
+// the same static number at each wait.
+template <class F>
+__global__ __launch_bounds__(kThreads) void mfma_px(const uint8_t *__restrict__ W, size_t pitch, int row0, int nrows,
+                                                    int nsb, const uint8_t *__restrict__ slabs,
+                                                    float *__restrict__ Y, int B) {
+    constexpr int CH = F::kChunks;
+    constexpr int CL = (kRowsPerWave * CH + 63) / 64;
+    constexpr int XI = (kSlabRows + kWaves - 1) / kWaves;  // slab rows per wave
+    __shared__ __align__(16) uint8_t sh_x[2][kSlabBytes];
+    __shared__ __align__(16) uint8_t sh_w[kWaves][kRowsPerWave * CH * 16];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, lr = lane & 31, kh = lane >> 5;
+    const int rbase = blockIdx.x * kRowsPerWG + wave * kRowsPerWave;
+    const int sb0 = 0, last = nsb - 1;
+    auto row_off = [&](int rho) { return (size_t)(row0 + min(rbase + rho, nrows - 1)) * pitch; };
+    size_t coff[CL];
+#pragma unroll
+    for (int k = 0; k < CL; k++) {
+        const int j = min(lane + 64 * k, kRowsPerWave * CH - 1);
+        coff[k] = row_off(j / CH) + 16 * (j % CH);
+    }
+    const size_t myoff = row_off(lr);
+    uint8_t *wslot = sh_w[wave];
+
+    // The slab DMA is issued from inline asm, outside the compiler's
+    // bookkeeping: its own waits would otherwise drain every load in flight
+    // before the first LDS read after a DMA.  Unknown memory operations can
+    // only make the compiler's remaining waits stricter, and the order below
+    // keeps them exact (each step's weight chunks are waited for before the
+    // step issues its DMA).
+    auto dma_x = [&](int sb, int buf) {
+        const uint8_t *src = slabs + (size_t)min(sb, last) * kSlabBytes + 16 * lane;
+        const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t *)sh_x[buf];
+#pragma unroll
+        for (int k = 0; k < XI; k++) {
+            const int r = min(wave + kWaves * k, kSlabRows - 1);  // surplus waves repeat the last row (same bytes)
+            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src + 1024 * r),
+                         "s"(dst + 1024 * r)
+                         : "memory", "m0");
+        }
+    };
+    u32x4 wa[CL], wb[CL];
+#define JH_LOAD_W(SET, SB)                                                                                 \
+    do {                                                                                                   \
+        const size_t sbo = (size_t)min((SB), last) * F::kBytes;                                            \
+        _Pragma("unroll") for (int k = 0; k < CL; k++)                                                     \
+            SET[k] = *reinterpret_cast<const u32x4 *>(W + ((coff[k] + sbo) & ~size_t(15)));                \
+    } while (0)
+
+    f32x16 tot[1] = {(f32x16){}};
+#define JH_STEP(SET, SB, BUF)                                                                              \
+    do {                                                                                                   \
+        /* this wave's part of slab SB and its chunks of SB have landed (only SB + 1's are in flight) */   \
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CL) : "memory");                                        \
+        _Pragma("unroll") for (int k = 0; k < CL; k++)                                                     \
+            if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot + 16 * (lane + 64 * k)) = SET[k]; \
+        /* every wave's part of slab SB is in, and every wave is done with slab SB - 1 */                \
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");                                   \
+        dma_x((SB) + 1, (BUF) ^ 1);                                                                        \
+        typename F::Regs w;                                                                                \
+        F::load(w, wslot + lr * CH * 16 + ((myoff + (size_t)(SB) * F::kBytes) & 15), kh);                 \
+        JH_LOAD_W(SET, (SB) + 2);                                                                          \
+        const CtxP c{lr, kh, sh_x[BUF]};                                                                   \
+        if constexpr (F::kSums) {                                                                          \
+            F::template compute<1>(w, c, tot);                                                             \
+        } else {                                                                                           \
+            f32x16 pt[1] = {(f32x16){}};                                                                   \
+            F::template compute<1>(w, c, pt);                                                              \
+            float S[16], cs[16];                                                                           \
+            col_terms<1>(c, 0, S, cs);                                                                     \
+            _Pragma("unroll") for (int i = 0; i < 16; i++) tot[0][i] = fmaf(cs[i], pt[0][i], tot[0][i]);   \
+        }                                                                                                  \
+    } while (0)
+
+    dma_x(sb0, 0);
+    JH_LOAD_W(wa, sb0);
+    JH_LOAD_W(wb, sb0 + 1);
+    int sb = sb0;
+    for (; sb < last; sb += 2) {  // pairs of steps: the register sets alternate by name
+        JH_STEP(wa, sb, 0);
+        JH_STEP(wb, sb + 1, 1);
+    }
+    if (sb == last) JH_STEP(wa, sb, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no DMA into LDS outlives the workgroup
+#undef JH_STEP
+#undef JH_LOAD_W
+
+    store_tile<1>(tot, rbase + lr, nrows, kh, B, Y, nullptr, nullptr, blockIdx.x, 0, 1);
 }
 
 }  // namespace
 
-static void mfma_split(int nrows, int nsb, int &tiles, int &ksplit, int &ksb) {
-    tiles = (nrows + kRowsPerWG - 1) / kRowsPerWG;
-    ksplit = (kMinWorkgroups + tiles - 1) / tiles;
-    if (ksplit > nsb) ksplit = nsb;
-    if (ksplit < 1) ksplit = 1;
-    ksb = (nsb + ksplit - 1) / ksplit;
-    ksplit = (nsb + ksb - 1) / ksb;
+// ------------------------------------------------------------------ host side
+static bool mfma_applies(const MfmaDesc &d, int B) {
+    if ((d.type != 12 && d.type != 13 && d.type != 14 && d.type != 8) || B < 16 || B > 64 || d.cols % 256 ||
+        d.cols <= 0 || d.row_end <= d.row_start)
+        return false;
+    if ((d.type == 12 || d.type == 13) && ((reinterpret_cast<uintptr_t>(d.w) | d.pitch) & 15))
+        return false;  // K-quant rows are staged as whole aligned 16-byte chunks
+    return (reinterpret_cast<uintptr_t>(d.x) & 15) == 0;  // x is read as float4
 }
 
-size_t mfma_workspace_bytes(int type, int B, int cols, int rows) {
-    if ((type != 12 && type != 13 && type != 14 && type != 8) || B < 16 || B > 64 || cols % 256 || rows < 1) return 0;
-    int tiles, ksplit, ksb;
-    mfma_split(rows, cols / 256, tiles, ksplit, ksb);
-    XWork w{(B + 31) / 32 * 32, cols, cols / 256, rows, ksplit, nullptr};
-    return w.bytes() > 256 ? w.bytes() : 256;  // nonzero: the MFMA path applies
-}
+namespace {
+struct Plan {
+    int nsb, ksb, ksplit, grid;
+    bool prepared;  // one unsplit matrix, B <= 32: x_prep + mfma_px
+    size_t slab_bytes, part_floats;
+};
+}  // namespace
 
-hipError_t launch_gemm_mfma_ws(const GemvArgs &a, void *workspace, hipStream_t s) {
-    if ((a.type != 12 && a.type != 13 && a.type != 14 && a.type != 8) || a.batch < 16 || a.batch > 64 || a.cols % 256)
-        return hipErrorNotSupported;
-    if ((a.type == 12 || a.type == 13) && ((reinterpret_cast<uintptr_t>(a.w) | a.pitch) & 15))
-        return hipErrorNotSupported;  // K-quant rows are staged as whole aligned 16-byte chunks
-    const int B = a.batch, Bp = (B + 31) / 32 * 32;
-    const int nrows = a.row_end - a.row_start;
-    const int nsb = a.cols / 256;
-    int tiles, ksplit, ksb;
-    mfma_split(nrows, nsb, tiles, ksplit, ksb);
-    XWork w{Bp, a.cols, nsb, nrows, ksplit, reinterpret_cast<uint8_t *>(workspace)};
-    dim3 grid(tiles, ksplit);
-#define JH_GEMM(F, NT) mfma_gemm<F, NT, NT == 1 ? kPrefetch : 1><<<grid, kThreads, 0, s>>>(a.w, a.pitch, a.row_start, nrows, nsb, ksb, w, a.x, a.y, B)
-    if (a.type == 12) {
-        if (Bp == 32) JH_GEMM(FmtQ4K, 1); else JH_GEMM(FmtQ4K, 2);
-    } else if (a.type == 13) {
-        if (Bp == 32) JH_GEMM(FmtQ5K, 1); else JH_GEMM(FmtQ5K, 2);
-    } else if (a.type == 14) {
-        if (Bp == 32) JH_GEMM(FmtQ6K, 1); else JH_GEMM(FmtQ6K, 2);
-    } else {
-        if (Bp == 32) JH_GEMM(FmtQ8_0, 1); else JH_GEMM(FmtQ8_0, 2);
+// Row tiles of 256 rows; K is split until the grid has kMinWorkgroups
+// workgroups (one per CU), with the same split for every matrix of the group.
+static bool plan_group(int n, const MfmaDesc *d, int B, Plan &p) {
+    if (n < 1 || n > kMaxMfmaGroup) return false;
+    int tiles = 0;
+    size_t rows = 0;
+    for (int i = 0; i < n; i++) {
+        if (!mfma_applies(d[i], B) || d[i].cols != d[0].cols) return false;
+        tiles += (d[i].row_end - d[i].row_start + kRowsPerWG - 1) / kRowsPerWG;
+        rows += d[i].row_end - d[i].row_start;
     }
-#undef JH_GEMM
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || ksplit == 1) return e;
-    const int n = B * nrows;
-    if (n % 4 == 0 && reinterpret_cast<uintptr_t>(a.y) % 16 == 0)
-        reduce_splits<float4><<<(unsigned)std::min((n / 4 + 255) / 256, 2048), 256, 0, s>>>(w, n / 4, ksplit, a.y);
-    else
-        reduce_splits<float><<<(unsigned)std::min((n + 255) / 256, 2048), 256, 0, s>>>(w, n, ksplit, a.y);
+    p.nsb = d[0].cols / 256;
+    int ks = (kMinWorkgroups + tiles - 1) / tiles;
+    ks = ks < 1 ? 1 : ks > p.nsb ? p.nsb : ks;
+    p.ksb = (p.nsb + ks - 1) / ks;
+    p.ksplit = (p.nsb + p.ksb - 1) / p.ksb;
+    if (p.ksplit > 1 && tiles > kMaxTileCounters) return false;
+    p.grid = tiles * p.ksplit;
+    p.prepared = n == 1 && p.ksplit == 1 && B <= 32;
+    p.slab_bytes = p.prepared ? (size_t)p.nsb * kSlabBytes : 0;
+    p.part_floats = p.ksplit > 1 ? (size_t)p.ksplit * B * rows : 0;
+    return true;
+}
+
+size_t mfma_group_workspace_bytes(int n, const MfmaDesc *d, int B) {
+    Plan p;
+    if (!plan_group(n, d, B, p)) return 0;
+    const size_t bytes = p.slab_bytes + p.part_floats * sizeof(float);
+    return bytes > 256 ? bytes : 256;  // nonzero: the MFMA path applies
+}
+
+template <int NT>
+static void launch_group_nt(const MfmaGroup &g, int mask, int grid, hipStream_t s) {
+    switch (mask) {
+        case 1: mfma_group<NT, 1><<<grid, kThreads, 0, s>>>(g); break;
+        case 2: mfma_group<NT, 2><<<grid, kThreads, 0, s>>>(g); break;
+        case 4: mfma_group<NT, 4><<<grid, kThreads, 0, s>>>(g); break;
+        case 8: mfma_group<NT, 8><<<grid, kThreads, 0, s>>>(g); break;
+        default: mfma_group<NT, 15><<<grid, kThreads, 0, s>>>(g); break;
+    }
+}
+
+hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, int *counters, hipStream_t s) {
+    Plan p;
+    if (!plan_group(n, d, B, p)) return hipErrorNotSupported;
+    if (p.ksplit > 1 && !counters) return hipErrorNotSupported;
+    uint8_t *ws = reinterpret_cast<uint8_t *>(workspace);
+    if (p.prepared) {
+        const MfmaDesc &m = d[0];
+        const int nrows = m.row_end - m.row_start;
+        x_prep<<<p.nsb, 512, 0, s>>>(m.x, B, m.cols, ws);
+#define JH_PX(F) mfma_px<F><<<p.grid, kThreads, 0, s>>>(m.w, m.pitch, m.row_start, nrows, p.nsb, ws, m.y, B)
+        if (m.type == 12) JH_PX(FmtQ4K);
+        else if (m.type == 13) JH_PX(FmtQ5K);
+        else if (m.type == 14) JH_PX(FmtQ6K);
+        else JH_PX(FmtQ8_0);
+#undef JH_PX
+        return hipGetLastError();
+    }
+    MfmaGroup g = {};
+    g.part = reinterpret_cast<float *>(ws);
+    g.counters = counters;
+    g.n = n;
+    g.nsb = p.nsb;
+    g.ksb = p.ksb;
+    g.ksplit = p.ksplit;
+    g.B = B;
+    int mask = 0, wg = 0, cnt = 0;
+    size_t part = 0;
+    for (int i = 0; i < n; i++) {
+        MfmaProblem &q = g.p[i];
+        q.w = d[i].w;
+        q.x = d[i].x;
+        q.y = d[i].y;
+        q.pitch = d[i].pitch;
+        q.type = d[i].type;
+        q.row0 = d[i].row_start;
+        q.rows = d[i].row_end - d[i].row_start;
+        q.tiles = (q.rows + kRowsPerWG - 1) / kRowsPerWG;
+        q.wg0 = wg;
+        q.cnt0 = cnt;
+        q.part0 = part;
+        wg += q.tiles * p.ksplit;
+        cnt += q.tiles;
+        part += p.ksplit > 1 ? (size_t)p.ksplit * B * q.rows : 0;
+        mask |= q.type == 12 ? 1 : q.type == 13 ? 2 : q.type == 14 ? 4 : 8;
+    }
+    if (B <= 32) launch_group_nt<1>(g, mask, p.grid, s);
+    else launch_group_nt<2>(g, mask, p.grid, s);
     return hipGetLastError();
 }
 

@@ -313,6 +313,17 @@ class HipMatVec:
         ys = (ctypes.c_void_p * max(n, 1))(*d_ys)
         _check(self._L.jh_qmatvec_group_dev(n, hs, xs, ys, stream or None))
 
+    def sgemv_batched_group_dev(self, mats, d_Xs, B: int, d_Ys, stream: int = 0) -> None:
+        """Y_i [B][rows_i] = X_i [B][cols] W_i^T for up to 4 matrices sharing cols:
+        one launch on the MFMA path (B >= 16), else one batched call per matrix."""
+        n = len(mats)
+        if not (len(d_Xs) == len(d_Ys) == n):
+            raise IllegalArgumentException("mats, X and Y must have the same length")
+        hs = (ctypes.c_void_p * max(n, 1))(*[m.handle for m in mats])
+        xs = (ctypes.c_void_p * max(n, 1))(*d_Xs)
+        ys = (ctypes.c_void_p * max(n, 1))(*d_Ys)
+        _check(self._L.jh_qmatvec_batched_group_dev(n, hs, xs, B, ys, stream or None))
+
     def dequantize_dev(self, A: DeviceQuantMatrix, d_out: int, stream: int = 0) -> None:
         _check(self._L.jh_qmat_dequant_dev(A.handle, d_out, stream or None))
 

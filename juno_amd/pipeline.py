@@ -10,8 +10,9 @@ Mirrors the reference's pipeline contract (paths under
 * ``forward_batch(request_ids, all_tokens, start_positions)``
   InferencePipeline.forwardBatch (:47-69): the reference's default is a serial
   loop over forward(); here the N requests are stacked and every layer runs
-  once for all of them (batched GEMVs: the B <= 8 GEMV kernel, fp16 MFMA from
-  B = 16; one batched rope + KV-append + attention launch pair)
+  once for all of them (batched GEMVs, [q, k, v] and [gate, up] grouped: the
+  B <= 8 GEMV kernel, fp16 MFMA from B = 16, one launch per group; one batched
+  rope + KV-append + attention launch pair)
 * ``vocab_size()``  InferencePipeline.vocabSize (:71-75)
 * ``evict(request_id)``  LlamaTransformerHandler.evict (:496-504)
 * ``lora``  an optional LoraAdapterSet whose "wq" / "wv" adapters are added after
@@ -144,14 +145,19 @@ class LlamaBatchPipeline:
         def gemv(m, x, y):
             _check(L.jh_qmatvec_batched_dev(m.handle, P(x), B, P(y), 0, m.rows, s))
 
+        def group(ms, x, ys):  # projections of one input: one launch on the MFMA path
+            n = len(ms)
+            hs = (_V * n)(*[m.handle for m in ms])
+            xs = (_V * n)(*[P(x)] * n)
+            yp = (_V * n)(*[P(y) for y in ys])
+            _check(L.jh_qmatvec_batched_group_dev(n, hs, xs, B, yp, s))
+
         _check(L.jh_embed_rows_dev(self.w.token_embd.handle, P(self.meta[0]), B, P(self.x), s))
         for li, lw in enumerate(self.w.layers):
             res = None if li == 0 else P(self.proj)  # previous layer's ffn output (:784)
             _check(L.jh_rmsnorm_rows_dev(P(self.x), res, P(lw.attn_norm), H, B, eps, P(self.x), P(self.xn), s))
             m = lw.mats
-            gemv(m["q"], self.xn, self.q)
-            gemv(m["k"], self.xn, self.k)
-            gemv(m["v"], self.xn, self.v)
+            group([m["q"], m["k"], m["v"]], self.xn, [self.q, self.k, self.v])
             if lw.bias is not None:  # addInPlace of the projection biases (LlamaTransformerHandler.java:758-761)
                 for name, out, n in (("q", self.q, H), ("k", self.k, KV), ("v", self.v, KV)):
                     _check(L.jh_add_rows_dev(P(out), P(lw.bias[name]), n, B, s))
@@ -167,8 +173,7 @@ class LlamaBatchPipeline:
             gemv(m["o"], self.att, self.proj)
             _check(L.jh_rmsnorm_rows_dev(P(self.x), P(self.proj), P(lw.ffn_norm), H, B, eps, P(self.x), P(self.xn),
                                          s))
-            gemv(m["gate"], self.xn, self.gate)
-            gemv(m["up"], self.xn, self.up)
+            group([m["gate"], m["up"]], self.xn, [self.gate, self.up])
             _check(L.jh_silu_mul_dev(P(self.gate), P(self.up), B * I, P(self.hid), s))
             gemv(m["down"], self.hid, self.proj)
         _check(L.jh_rmsnorm_rows_dev(P(self.x), P(self.proj), P(self.w.output_norm), H, B, eps, P(self.x),

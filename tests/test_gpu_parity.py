@@ -307,6 +307,83 @@ def test_batched_mfma_odd_pitch_row_range(be, qtype):
                 assert rel_err(Y[j], ref, deq[a:b], X[j]).max() <= TOL, (a, b, j)
 
 
+@pytest.mark.parametrize("qtype,rows,B", [(O.Q4_K, 1024, 32), (O.Q6_K, 4096, 20), (O.Q8_0, 3072, 48)])
+def test_batched_mfma_split_graph_replay(be, qtype, rows, B):
+    """Split-K tiles hand their partials to the last-arriving split through
+    per-tile counters that every launch re-arms: eager launches and HIP-graph
+    replays (with other eager work between them) are bit-identical, and match
+    the oracle to the GEMV bar."""
+    import ctypes
+    import torch
+    from juno_amd import _lib
+    L = _lib.load()
+    cols = 4096
+    raw = O.quantize(qtype, weights(rows * cols, 600 + rows))
+    deq = O.dequantize(qtype, raw, rows, cols)
+    X = vec(cols, 601, batch=B)
+    with upload(be, qtype, raw, rows, cols) as dev:
+        s = torch.cuda.Stream()
+        dx = torch.from_numpy(X).cuda()
+        dy = torch.zeros(B, rows, device="cuda")
+        S = ctypes.c_void_p(s.cuda_stream)
+
+        def launch():
+            assert L.jh_qmatvec_batched_dev(dev.handle, ctypes.c_void_p(dx.data_ptr()), B,
+                                            ctypes.c_void_p(dy.data_ptr()), 0, rows, S) == 0
+
+        with torch.cuda.stream(s):
+            launch()
+        s.synchronize()
+        eager = dy.cpu().numpy()
+        for j in (0, B - 1):
+            ref = O.matvec(qtype, raw, X[j], 0, rows, cols).astype(np.float64)
+            assert rel_err(eager[j], ref, deq, X[j]).max() <= TOL, j
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                launch()
+        for rep in range(3):
+            say("mfma graph replay", qtype, rows, B, rep)
+            dy.zero_()
+            with torch.cuda.stream(s):
+                g.replay()
+            s.synchronize()
+            assert np.array_equal(dy.cpu().numpy(), eager), rep
+            with torch.cuda.stream(s):
+                launch()  # eager work between replays
+            s.synchronize()
+            assert np.array_equal(dy.cpu().numpy(), eager), rep
+
+
+@pytest.mark.parametrize("B", [16, 20, 32, 48])
+def test_batched_group_mixed_formats(be, B):
+    """jh_qmatvec_batched_group_dev: Q4_K q / k and a Q6_K v sharing cols (a
+    Q4_K_M attention group) plus a Q8_0 matrix with its own x, one launch;
+    every output against the oracle to the GEMV bar, and a row count that is
+    not a multiple of the tile."""
+    import torch
+    cols = 2048
+    spec = [(O.Q4_K, 1024, 0), (O.Q4_K, 256, 0), (O.Q6_K, 333, 0), (O.Q8_0, 512, 1)]
+    Xs = [vec(cols, 700 + B, batch=B), vec(cols, 701 + B, batch=B)]
+    raws = [O.quantize(t, weights(r * cols, 710 + i)) for i, (t, r, _) in enumerate(spec)]
+    devs = [upload(be, t, raw, r, cols) for (t, r, _), raw in zip(spec, raws)]
+    try:
+        dX = [torch.from_numpy(X).cuda() for X in Xs]
+        dY = [torch.full((B, r), float("nan"), device="cuda") for _, r, _ in spec]
+        say("batched group", B)
+        be.sgemv_batched_group_dev(devs, [dX[xi].data_ptr() for _, _, xi in spec], B, [y.data_ptr() for y in dY])
+        torch.cuda.synchronize()
+        for (t, r, xi), raw, y in zip(spec, raws, dY):
+            Y = y.cpu().numpy()
+            deq = O.dequantize(t, raw, r, cols)
+            for j in (0, B // 2, B - 1):
+                ref = O.matvec(t, raw, Xs[xi][j], 0, r, cols).astype(np.float64)
+                assert rel_err(Y[j], ref, deq, Xs[xi][j]).max() <= TOL, (t, r, j)
+    finally:
+        for d in devs:
+            d.close()
+
+
 def test_batched_row_range(be):
     rows, cols, B = 700, 1024, 16
     raw = O.quantize(O.Q4_K, weights(rows * cols, 70))
