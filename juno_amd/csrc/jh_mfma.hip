@@ -171,14 +171,17 @@ struct CtxP {
 // lanes store consecutive rows.
 __device__ __forceinline__ int batch_of(int n, int i, int kh) { return n * 32 + 8 * (i >> 2) + 4 * kh + (i & 3); }
 
-// four byte pairs of two words -> 16-bit lanes, OR'ed into fp16 1024 + u
+// four byte pairs of two words -> fp16 1024 + u in 16-bit lanes: one byte
+// permute per pair takes u from the word and the exponent byte 0x64 from a
+// constant second source
 __device__ __forceinline__ half8 bytes_to_h8(uint32_t w0, uint32_t w1, half2v off) {
-    const uint32_t p[4] = {__builtin_amdgcn_perm(0u, w0, 0x0C010C00u), __builtin_amdgcn_perm(0u, w0, 0x0C030C02u),
-                           __builtin_amdgcn_perm(0u, w1, 0x0C010C00u), __builtin_amdgcn_perm(0u, w1, 0x0C030C02u)};
+    const uint32_t e = 0x64646464u;
+    const uint32_t p[4] = {__builtin_amdgcn_perm(e, w0, 0x04010400u), __builtin_amdgcn_perm(e, w0, 0x04030402u),
+                           __builtin_amdgcn_perm(e, w1, 0x04010400u), __builtin_amdgcn_perm(e, w1, 0x04030402u)};
     half8 a;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const half2v h = __builtin_bit_cast(half2v, p[j] | 0x64006400u) - off;  // exact: small integers
+        const half2v h = __builtin_bit_cast(half2v, p[j]) - off;  // exact: small integers
         a[2 * j] = h[0];
         a[2 * j + 1] = h[1];
     }
