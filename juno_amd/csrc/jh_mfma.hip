@@ -216,6 +216,33 @@ __device__ __forceinline__ void col_terms(const C &c, int n, float (&S)[16], flo
         }
 }
 
+// N dwords at a 2-byte-aligned LDS address, read as aligned dwords and
+// realigned in registers with v_alignbyte.  Unaligned 8- and 16-byte LDS reads
+// stall the LDS pipeline (and the x-fragment reads queued behind them).  One
+// dword past the field is read and ignored when p is dword-aligned, so the
+// weight windows end with kWinPad bytes of padding.
+constexpr int kWinPad = 16;
+template <int N>
+__device__ __forceinline__ void lds_read_u(const uint8_t *p, uint32_t (&out)[N]) {
+    const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3);
+    const uint32_t *b = reinterpret_cast<const uint32_t *>(p - sh);
+    uint32_t w[N + 1];
+#pragma unroll
+    for (int i = 0; i <= N; i++) w[i] = b[i];
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
+}
+__device__ __forceinline__ u32x2 lds_u32x2(const uint8_t *p) {
+    uint32_t v[2];
+    lds_read_u<2>(p, v);
+    return u32x2{v[0], v[1]};
+}
+__device__ __forceinline__ u32x4 lds_u32x4(const uint8_t *p) {
+    uint32_t v[4];
+    lds_read_u<4>(p, v);
+    return u32x4{v[0], v[1], v[2], v[3]};
+}
+
 // Q4_K (matVecQ4Kraw, LlamaTransformerHandler.java:1428-1468): w = d*ls*q - dmin*lm.
 // B = 1024 + ls*q (<= 1969, exact), built with one 24-bit multiply-add per
 // pair; 1024 * sum(x) and the min term (one more MFMA: A = [sub-block sums
@@ -234,6 +261,7 @@ struct FmtKQ {
         u32x2 qp[4][2];
         u32x2 qh[2];  // Q5_K: qh bytes 16 j + 8 kh .. +8 (bit s for sub-block s)
     };
+    template <bool RA>  // rows are 16-byte aligned: the reads are aligned either way
     static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
         r.hd = *reinterpret_cast<const u32x4 *>(p);
 #pragma unroll
@@ -327,17 +355,26 @@ struct FmtQ6K {
         u32x4 sc;           // bytes 192..207
         uint32_t dw;        // bytes 206..209: d in the high half
     };
+    template <bool RA>  // realign in registers (aligned LDS reads) or read the 2-byte-aligned fields directly
     static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
 #pragma unroll
         for (int n = 0; n < 2; n++)
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                r.ql[n][0][j] = *reinterpret_cast<const u32x2a2 *>(p + 64 * n + 16 * j + 8 * kh);
-                r.ql[n][1][j] = *reinterpret_cast<const u32x2a2 *>(p + 64 * n + 32 + 16 * j + 8 * kh);
-                r.qh[n][j] = *reinterpret_cast<const u32x2a2 *>(p + 128 + 32 * n + 16 * j + 8 * kh);
+                const uint8_t *a = p + 64 * n + 16 * j + 8 * kh, *h = p + 128 + 32 * n + 16 * j + 8 * kh;
+                r.ql[n][0][j] = RA ? lds_u32x2(a) : *reinterpret_cast<const u32x2a2 *>(a);
+                r.ql[n][1][j] = RA ? lds_u32x2(a + 32) : *reinterpret_cast<const u32x2a2 *>(a + 32);
+                r.qh[n][j] = RA ? lds_u32x2(h) : *reinterpret_cast<const u32x2a2 *>(h);
             }
-        r.sc = *reinterpret_cast<const u32x4a2 *>(p + 192);
-        r.dw = *reinterpret_cast<const u32a2 *>(p + 206);
+        if (RA) {
+            r.sc = lds_u32x4(p + 192);
+            uint32_t dw[1];
+            lds_read_u<1>(p + 206, dw);
+            r.dw = dw[0];
+        } else {
+            r.sc = *reinterpret_cast<const u32x4a2 *>(p + 192);
+            r.dw = *reinterpret_cast<const u32a2 *>(p + 206);
+        }
     }
     template <int NT, class C>
     static __device__ __forceinline__ void compute(const Regs &r, const C &c, f32x16 *tot) {
@@ -373,10 +410,12 @@ struct FmtQ8_0 {
         u32x4 q[8];     // block b: bytes 34b + 2 + 16kh .. +16
         uint32_t d[8];  // d of block b (low half)
     };
+    template <bool RA>
     static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
 #pragma unroll
         for (int b = 0; b < 8; b++) {
-            r.q[b] = *reinterpret_cast<const u32x4a2 *>(p + 34 * b + 2 + 16 * kh);
+            const uint8_t *a = p + 34 * b + 2 + 16 * kh;
+            r.q[b] = RA ? lds_u32x4(a) : *reinterpret_cast<const u32x4a2 *>(a);
             r.d[b] = *reinterpret_cast<const uint16_t *>(p + 34 * b);
         }
     }
@@ -525,7 +564,9 @@ __host__ __device__ constexpr int max_chunks() {
 template <int NT>
 __host__ __device__ constexpr int lds_w_offset() { return (2 * 32 * NT * COLH + 32 * NT * 16) * 2 + 32 * NT * 8; }
 template <int NT, int MASK>
-__host__ __device__ constexpr int lds_bytes() { return lds_w_offset<NT>() + kWaves * kRowsPerWave * max_chunks<MASK>() * 16; }
+__host__ __device__ constexpr int lds_bytes() {
+    return lds_w_offset<NT>() + kWaves * kRowsPerWave * max_chunks<MASK>() * 16 + kWinPad;
+}
 
 // One workgroup's tile (32 rows per wave x all batch columns) over the K
 // range of its split, x converted into LDS super-block by super-block.
@@ -604,7 +645,7 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
             if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot + 16 * (lane + 64 * k)) = ch_n[0][k];
         // this lane's row block inside its staged window (same wave: no barrier)
         typename F::Regs w;
-        F::load(w, wslot + c.lr * CH * 16 + ((myoff + (size_t)sb * F::kBytes) & 15), c.kh);
+        F::template load<NT == 1>(w, wslot + c.lr * CH * 16 + ((myoff + (size_t)sb * F::kBytes) & 15), c.kh);
         // the loads below overlap this super-block's math
         if (sb + 1 < sb1) JH_LOAD_X(sb + 1);
 #pragma unroll
@@ -747,7 +788,7 @@ __global__ __launch_bounds__(kThreads) void mfma_px(const uint8_t *__restrict__ 
     constexpr int CL = (kRowsPerWave * CH + 63) / 64;
     constexpr int XI = (kSlabRows + kWaves - 1) / kWaves;  // slab rows per wave
     __shared__ __align__(16) uint8_t sh_x[2][kSlabBytes];
-    __shared__ __align__(16) uint8_t sh_w[kWaves][kRowsPerWave * CH * 16];
+    __shared__ __align__(16) uint8_t sh_w[kWaves * kRowsPerWave * CH * 16 + kWinPad];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, lr = lane & 31, kh = lane >> 5;
@@ -761,7 +802,7 @@ __global__ __launch_bounds__(kThreads) void mfma_px(const uint8_t *__restrict__ 
         coff[k] = row_off(j / CH) + 16 * (j % CH);
     }
     const size_t myoff = row_off(lr);
-    uint8_t *wslot = sh_w[wave];
+    uint8_t *wslot = sh_w + wave * (kRowsPerWave * CH * 16);
 
     // The slab DMA is issued from inline asm, outside the compiler's
     // bookkeeping: its own waits would otherwise drain every load in flight
@@ -799,7 +840,7 @@ __global__ __launch_bounds__(kThreads) void mfma_px(const uint8_t *__restrict__ 
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");                                   \
         dma_x((SB) + 1, (BUF) ^ 1);                                                                        \
         typename F::Regs w;                                                                                \
-        F::load(w, wslot + lr * CH * 16 + ((myoff + (size_t)(SB) * F::kBytes) & 15), kh);                 \
+        F::template load<true>(w, wslot + lr * CH * 16 + ((myoff + (size_t)(SB) * F::kBytes) & 15), kh);  \
         JH_LOAD_W(SET, (SB) + 2);                                                                          \
         const CtxP c{lr, kh, sh_x[BUF]};                                                                   \
         if constexpr (F::kSums) {                                                                          \
