@@ -243,6 +243,11 @@ __device__ __forceinline__ u32x4 lds_u32x4(const uint8_t *p) {
     return u32x4{v[0], v[1], v[2], v[3]};
 }
 
+// Window position (in chunks) of chunk j of a wave's 32 x CH chunk grid when
+// rows are RC >= CH chunks apart.
+template <int CH, int RC>
+__device__ __forceinline__ int win_chunk(int j) { return RC == CH ? j : j + (RC - CH) * (j / CH); }
+
 // Q4_K (matVecQ4Kraw, LlamaTransformerHandler.java:1428-1468): w = d*ls*q - dmin*lm.
 // B = 1024 + ls*q (<= 1969, exact), built with one 24-bit multiply-add per
 // pair; 1024 * sum(x) and the min term (one more MFMA: A = [sub-block sums
@@ -254,6 +259,7 @@ template <bool Q5>
 struct FmtKQ {
     static constexpr int kBytes = Q5 ? 176 : 144;
     static constexpr int kChunks = kBytes / 16;  // rows are 16-byte aligned (pitch kBytes * n, aligned base)
+    static constexpr int kRowChunks = kChunks;   // LDS window row stride (16-byte chunks)
     static constexpr int kQs = Q5 ? 48 : 16;
     static constexpr bool kSums = true;
     struct Regs {
@@ -348,6 +354,9 @@ using FmtQ5K = FmtKQ<true>;
 struct FmtQ6K {
     static constexpr int kBytes = 210;
     static constexpr int kChunks = (kBytes + 14 + 15) / 16;  // a 2-byte-aligned block spans <= 14 chunks
+    // window rows 15 chunks (60 dwords) apart: the dword reads of 32 rows hit 16
+    // banks (2-way) instead of the 8 of a 56-dword stride
+    static constexpr int kRowChunks = kChunks + 1;
     static constexpr bool kSums = false;
     struct Regs {
         u32x2 ql[2][2][2];  // [half n][ql +32 p][j]: bytes 64n + 32p + 16j + 8kh
@@ -405,6 +414,7 @@ struct FmtQ6K {
 struct FmtQ8_0 {
     static constexpr int kBytes = 8 * 34;
     static constexpr int kChunks = (kBytes + 14 + 15) / 16;
+    static constexpr int kRowChunks = kChunks + 1;  // 76-dword window rows (see FmtQ6K)
     static constexpr bool kSums = false;
     struct Regs {
         u32x4 q[8];     // block b: bytes 34b + 2 + 16kh .. +16
@@ -554,10 +564,10 @@ struct MfmaGroup {
 template <int MASK>
 __host__ __device__ constexpr int max_chunks() {
     int c = 0;
-    if (MASK & 1) c = c > FmtQ4K::kChunks ? c : FmtQ4K::kChunks;
-    if (MASK & 2) c = c > FmtQ5K::kChunks ? c : FmtQ5K::kChunks;
-    if (MASK & 4) c = c > FmtQ6K::kChunks ? c : FmtQ6K::kChunks;
-    if (MASK & 8) c = c > FmtQ8_0::kChunks ? c : FmtQ8_0::kChunks;
+    if (MASK & 1) c = c > FmtQ4K::kRowChunks ? c : FmtQ4K::kRowChunks;
+    if (MASK & 2) c = c > FmtQ5K::kRowChunks ? c : FmtQ5K::kRowChunks;
+    if (MASK & 4) c = c > FmtQ6K::kRowChunks ? c : FmtQ6K::kRowChunks;
+    if (MASK & 8) c = c > FmtQ8_0::kRowChunks ? c : FmtQ8_0::kRowChunks;
     return c;
 }
 // LDS image: [x hi: BP x COLH][x lo: BP x COLH][sums: BP x 16 halves][(S, 1/s): BP][weight windows]
@@ -602,7 +612,8 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
         coff[k] = row_off(j / CH) + 16 * (j % CH);
     }
     const size_t myoff = row_off(c.lr);
-    uint8_t *wslot = lds + lds_w_offset<NT>() + wave * (kRowsPerWave * CH * 16);
+    constexpr int RC = NT == 1 ? F::kRowChunks : CH;  // window row stride (chunks): padded for the realigned reads
+    uint8_t *wslot = lds + lds_w_offset<NT>() + wave * (kRowsPerWave * RC * 16);
 
     u32x4 ch_n[PD][CL];
     float xv_n[CPT][16];  // the next super-block's raw x: column (threadIdx.x >> 4) + 32 i, values 16 q .. +16
@@ -642,10 +653,10 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
             stage_x_column(xv_n[i], xq, sh_hi, sh_lo, sh_xs, sh_S, xcol + 32 * i, COLH);
 #pragma unroll
         for (int k = 0; k < CL; k++)
-            if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot + 16 * (lane + 64 * k)) = ch_n[0][k];
+            if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot + 16 * win_chunk<CH, RC>(lane + 64 * k)) = ch_n[0][k];
         // this lane's row block inside its staged window (same wave: no barrier)
         typename F::Regs w;
-        F::template load<NT == 1>(w, wslot + c.lr * CH * 16 + ((myoff + (size_t)sb * F::kBytes) & 15), c.kh);
+        F::template load<NT == 1>(w, wslot + c.lr * RC * 16 + ((myoff + (size_t)sb * F::kBytes) & 15), c.kh);
         // the loads below overlap this super-block's math
         if (sb + 1 < sb1) JH_LOAD_X(sb + 1);
 #pragma unroll
@@ -788,7 +799,8 @@ __global__ __launch_bounds__(kThreads) void mfma_px(const uint8_t *__restrict__ 
     constexpr int CL = (kRowsPerWave * CH + 63) / 64;
     constexpr int XI = (kSlabRows + kWaves - 1) / kWaves;  // slab rows per wave
     __shared__ __align__(16) uint8_t sh_x[2][kSlabBytes];
-    __shared__ __align__(16) uint8_t sh_w[kWaves * kRowsPerWave * CH * 16 + kWinPad];
+    constexpr int RC = F::kRowChunks;  // window row stride (chunks)
+    __shared__ __align__(16) uint8_t sh_w[kWaves * kRowsPerWave * RC * 16 + kWinPad];
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, lr = lane & 31, kh = lane >> 5;
@@ -802,7 +814,7 @@ __global__ __launch_bounds__(kThreads) void mfma_px(const uint8_t *__restrict__ 
         coff[k] = row_off(j / CH) + 16 * (j % CH);
     }
     const size_t myoff = row_off(lr);
-    uint8_t *wslot = sh_w + wave * (kRowsPerWave * CH * 16);
+    uint8_t *wslot = sh_w + wave * (kRowsPerWave * RC * 16);
 
     // The slab DMA is issued from inline asm, outside the compiler's
     // bookkeeping: its own waits would otherwise drain every load in flight
@@ -835,12 +847,12 @@ __global__ __launch_bounds__(kThreads) void mfma_px(const uint8_t *__restrict__ 
         /* this wave's part of slab SB and its chunks of SB have landed (only SB + 1's are in flight) */   \
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CL) : "memory");                                        \
         _Pragma("unroll") for (int k = 0; k < CL; k++)                                                     \
-            if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot + 16 * (lane + 64 * k)) = SET[k]; \
+            if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot + 16 * win_chunk<CH, RC>(lane + 64 * k)) = SET[k]; \
         /* every wave's part of slab SB is in, and every wave is done with slab SB - 1 */                \
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");                                   \
         dma_x((SB) + 1, (BUF) ^ 1);                                                                        \
         typename F::Regs w;                                                                                \
-        F::template load<true>(w, wslot + lr * CH * 16 + ((myoff + (size_t)(SB) * F::kBytes) & 15), kh);  \
+        F::template load<true>(w, wslot + lr * RC * 16 + ((myoff + (size_t)(SB) * F::kBytes) & 15), kh);  \
         JH_LOAD_W(SET, (SB) + 2);                                                                          \
         const CtxP c{lr, kh, sh_x[BUF]};                                                                   \
         if constexpr (F::kSums) {                                                                          \
