@@ -310,6 +310,61 @@ def measured_traffic():
         return None, None
 
 
+def decode_step_8b(torch, be, stream, steps, mats, B):
+    """Full decode steps at the Llama-3-8B shape (32 layers, hidden 4096, 32 / 8
+    heads of 128, FFN 14336, vocab 128256, rope theta 500000) on the bench's own
+    packed matrices, with N(0.5..1.5) norm weights and a Q6_K token embedding:
+    B = 1 through LlamaDecoder (from the residual stream), B > 1 through
+    LlamaBatchPipeline (token rows, one step for all B requests).  Every request
+    is at position 511 over a KV cache pre-filled with N(0, 1); the step is one
+    captured graph.  Every op of the step is a HIP kernel."""
+    from juno_amd import decode as D
+    from juno_amd.pipeline import LlamaBatchPipeline
+    cfg = D.LlamaConfig(hidden_dim=HIDDEN, num_layers=LAYERS, num_heads=32, num_kv_heads=8, head_dim=128,
+                        intermediate_size=FFN, vocab_size=VOCAB, rms_norm_eps=1e-5, rope_theta=500000.0)
+    by = {m[0]: m[4] for m in mats}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(10)
+    norm = lambda: torch.rand(HIDDEN, generator=g, device="cuda").add_(0.5)
+    names = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output", "gate": "ffn_gate", "up": "ffn_up",
+             "down": "ffn_down"}
+    layers = [D.LlamaLayerWeights(norm(), norm(), {k: by[f"blk.{l}.{v}"] for k, v in names.items()})
+              for l in range(LAYERS)]
+    emb = None
+    if B > 1:
+        src = torch.randn(VOCAB * HIDDEN, generator=g, device="cuda")
+        emb = be.quantize_dev(Q6_K, src.data_ptr(), VOCAB, HIDDEN, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        del src
+    w = D.LlamaWeights(cfg, layers, norm(), by["output"], token_embd=emb)
+    if B == 1:
+        dec = D.LlamaDecoder(w, max_seq=512)
+        dec.k_cache.normal_(generator=g)
+        dec.v_cache.normal_(generator=g)
+        dec.x.normal_(generator=g)
+        dec.pos.fill_(511)
+        x0 = dec.x.clone()
+
+        def full():
+            dec.x.copy_(x0)  # the step updates the residual stream in place
+            dec.enqueue_step(stream)
+        ms, _ = time_graph(torch, full, stream, steps, 3)
+        del dec
+    else:
+        pipe = LlamaBatchPipeline(w, max_seq=512, max_batch=B)
+        pipe.k_cache.normal_(generator=g)
+        pipe.v_cache.normal_(generator=g)
+        pipe.meta.copy_(torch.tensor([[(97 * b) % VOCAB for b in range(B)], [511] * B, list(range(B))],
+                                     dtype=torch.int32))
+        ms, _ = time_graph(torch, lambda: pipe.enqueue(B, stream), stream, steps, 3)
+        del pipe
+    if emb is not None:
+        emb.close()
+    torch.cuda.synchronize()
+    return {"config": f"llama3-8b-q4_k_m-full-decode-step-b{B}-ctx512", "batch": B, "ms_per_step": round(ms, 4),
+            "tok_s": round(B * 1e3 / ms, 1)}
+
+
 def tinyllama_step(torch, stream, steps):
     """TinyLlama-1.1B-shaped Q4_K_M full decode step (22 layers,
     hidden 2048, 32 / 4 heads, head_dim 64, FFN 5632, vocab 32000; Q6_K for
@@ -377,7 +432,7 @@ def tinyllama_batch_step(torch, stream, steps, w, cfg, B):
     del pipe
     return {"config": f"tinyllama-1.1b-q4_k_m-forward-batch-b{B}-ctx512", "batch": B, "ms_per_step": round(ms, 4),
             "tok_s": round(B * 1e3 / ms, 1),
-            "launches_per_step": cfg.num_layers * 12 + 3}
+            "launches_per_step": cfg.num_layers * 9 + 3}
 
 
 def main():
@@ -435,6 +490,12 @@ def main():
                    "GB_s": round(sb32 / (ms32 * 1e-3) / 1e9, 1)}
         log(f"B=32 step: {ms32:.4f} ms  {batched}")
 
+    full8b = {"b1": decode_step_8b(torch, be, stream, max(args.steps // 2, 10), mats, 1)}
+    log(f"8B full decode step, B=1: {full8b['b1']}")
+    if not args.no_batched:
+        full8b["b32"] = decode_step_8b(torch, be, stream, max(args.steps // 5, 3), mats, 32)
+        log(f"8B full decode step, B=32: {full8b['b32']}")
+
     tiny = tinyllama_step(torch, stream, max(args.steps // 2, 10))
     log(f"TinyLlama decode step: {tiny}")
 
@@ -473,6 +534,7 @@ def main():
                      "algorithmic_bytes_per_launch": per_launch},
         "cpu_baseline": cpu,
         "batched": batched,
+        "decode_step_8b": full8b,
         "decode_step_tinyllama": tiny,
         "parity_max_rel_err": parity,
         "device": info["name"],
