@@ -111,6 +111,13 @@ __device__ __forceinline__ void rope_pair(float &x0, float &x1, int p, int head_
     x1 = y1;
 }
 
+// rope_pair's rotation with its (cos, sin) already formed
+__device__ __forceinline__ void rope_rot(float &x0, float &x1, float c, float s) {
+    const float y0 = x0 * c - x1 * s, y1 = x0 * s + x1 * c;
+    x0 = y0;
+    x1 = y1;
+}
+
 // chunk length: one position per lane, fewer for wide heads (LDS holds the
 // chunk's K and V)
 __host__ __device__ constexpr int attn_tc(int head_dim) { return head_dim <= 128 ? 64 : 32; }
@@ -224,6 +231,156 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_k(
             ph[1] = l;
         }
         // sq / sp are rewritten by this wave's next head
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
+// attn_chunk_k for head_dim HD in {64, 128} (Llama, TinyLlama, Qwen2): the
+// same work split and results up to summation order, with the per-lane loops
+// unrolled into independent chains.  K rows sit in LDS as float4 slots,
+// XOR-swizzled per row (slot j of row t at j ^ (t mod HD/4)), so that a lane
+// reads its row 16 bytes at a time and the 16 lanes of an LDS pass hit distinct
+// banks; q . k runs in four accumulators.  For p . V each lane owns HD / 64
+// adjacent output dims and alternates two accumulators over positions.
+template <bool FUSED, int HD>
+__global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
+    const float *__restrict__ q, const float *__restrict__ k_new, const float *__restrict__ v_new,
+    float *__restrict__ k_cache, float *__restrict__ v_cache, int n_heads, int n_kv_heads, const int *__restrict__ d_pos,
+    int max_seq, float theta, float scale, float *__restrict__ part, const int *__restrict__ d_slot, int n_slots) {
+    constexpr int tc = attn_tc(HD), Q4 = HD / 4, M = Q4 - 1, DPL = HD / 64;
+    extern __shared__ float lds[];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    float4 *sk4 = reinterpret_cast<float4 *>(lds);  // [tc][Q4] swizzled
+    float *sv = lds + tc * HD;                        // [tc][HD]
+    float *srope = sv + tc * HD;                      // [HD / 2] (cos, sin) of this request's position
+    float *sq = srope + HD + wave * (HD + tc);        // this wave's [HD] q, then [tc] weights
+    float *sp = sq + HD;
+    const int z = blockIdx.z, kv_dim = n_kv_heads * HD;
+    q += (size_t)z * n_heads * HD;
+    if (FUSED) {
+        k_new += (size_t)z * kv_dim;
+        v_new += (size_t)z * kv_dim;
+    }
+    {
+        const size_t cb = d_slot ? (size_t)min(max(d_slot[z], 0), n_slots - 1) * max_seq * kv_dim : 0;
+        k_cache += cb;
+        v_cache += cb;
+    }
+    part += (size_t)z * n_heads * gridDim.y * (HD + 2);
+    const int pos = min(d_pos[z], max_seq - 1), T = pos + 1;
+    const int g = blockIdx.x, c = blockIdx.y, t0 = c * tc;
+    if (t0 >= T) return;  // uniform across the workgroup
+    const int R = n_heads / n_kv_heads;
+    const int nt = min(tc, T - t0);
+    const bool has_pos = FUSED && pos < t0 + tc;
+    // four rows' loads in flight per thread before any is written (rows past
+    // the chunk's end or the cache are clamped for the load and not written)
+    for (int base = 0; base < nt * Q4; base += 4 * (int)blockDim.x) {
+        float4 kk[4], vv[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = base + u * blockDim.x + threadIdx.x, t = i / Q4, j = i % Q4;
+            const size_t o = (size_t)min(t0 + t, T - 1) * kv_dim + g * HD + 4 * j;
+            kk[u] = *reinterpret_cast<const float4 *>(k_cache + o);
+            vv[u] = *reinterpret_cast<const float4 *>(v_cache + o);
+        }
+        // rope's (cos, sin) for this position, once per workgroup, while the first loads are in flight
+        // (rope_pair's arithmetic: the same values)
+        if (FUSED && base == 0 && threadIdx.x < HD / 2) {
+            const int pp = threadIdx.x;
+            const double freq = 1.0 / pow((double)theta, (2.0 * pp) / HD);
+            const double angle = pos * freq;
+            srope[2 * pp] = (float)cos(angle);
+            srope[2 * pp + 1] = (float)sin(angle);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = base + u * blockDim.x + threadIdx.x, t = i / Q4, j = i % Q4;
+            if (t >= nt || (has_pos && t0 + t == pos)) continue;
+            sk4[t * Q4 + (j ^ (t & M))] = kk[u];
+            *reinterpret_cast<float4 *>(sv + t * HD + 4 * j) = vv[u];
+        }
+    }
+    if (has_pos) {
+        const int tp = pos - t0;
+        float *skf = reinterpret_cast<float *>(sk4);
+        for (int p = threadIdx.x; p < HD / 2; p += blockDim.x) {  // thread p wrote pair p of the table
+            float ka = k_new[g * HD + 2 * p], kb = k_new[g * HD + 2 * p + 1];
+            rope_rot(ka, kb, srope[2 * p], srope[2 * p + 1]);
+            const int d = 2 * p, slot = tp * Q4 + ((d >> 2) ^ (tp & M));
+            skf[4 * slot + (d & 3)] = ka;
+            skf[4 * slot + (d & 3) + 1] = kb;
+            const size_t o = (size_t)pos * kv_dim + g * HD + 2 * p;
+            k_cache[o] = ka;
+            k_cache[o + 1] = kb;
+        }
+        for (int d = threadIdx.x; d < HD; d += blockDim.x) {
+            const float v = v_new[g * HD + d];
+            sv[tp * HD + d] = v;
+            v_cache[(size_t)pos * kv_dim + g * HD + d] = v;
+        }
+    }
+    __syncthreads();
+    for (int r = wave; r < R; r += nw) {  // wave-uniform
+        const int h = g * R + r;
+        for (int p = lane; p < HD / 2; p += 64) {
+            float a = q[h * HD + 2 * p], b = q[h * HD + 2 * p + 1];
+            if (FUSED) rope_rot(a, b, srope[2 * p], srope[2 * p + 1]);
+            sq[2 * p] = a;
+            sq[2 * p + 1] = b;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // lanes past the chunk's end compute on whatever row lane holds and are masked
+        const float4 *q4 = reinterpret_cast<const float4 *>(sq);
+        const float4 *k4 = sk4 + lane * Q4;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+        for (int j = 0; j < Q4; j++) {
+            const float4 qq = q4[j], kk = k4[j ^ (lane & M)];
+            a0 = fmaf(qq.x, kk.x, a0);
+            a1 = fmaf(qq.y, kk.y, a1);
+            a2 = fmaf(qq.z, kk.z, a2);
+            a3 = fmaf(qq.w, kk.w, a3);
+        }
+        const float s = lane < nt ? ((a0 + a1) + (a2 + a3)) * scale : -INFINITY;
+        float m = s;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float e = lane < nt ? (float)exp((double)(s - m)) : 0.f;
+        const float l = wave_sum(e);
+        if (lane < tc) sp[lane] = e;  // one weight per position (0 past the chunk's end)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float oe[DPL], oo[DPL];
+#pragma unroll
+        for (int i = 0; i < DPL; i++) oe[i] = oo[i] = 0.f;
+        const float *vcol = sv + DPL * lane;
+        int t = 0;
+        for (; t + 1 < nt; t += 2) {
+            const float pe = sp[t], po = sp[t + 1];
+#pragma unroll
+            for (int i = 0; i < DPL; i++) {
+                oe[i] = fmaf(pe, vcol[t * HD + i], oe[i]);
+                oo[i] = fmaf(po, vcol[(t + 1) * HD + i], oo[i]);
+            }
+        }
+        if (t < nt) {
+            const float pe = sp[t];
+#pragma unroll
+            for (int i = 0; i < DPL; i++) oe[i] = fmaf(pe, vcol[t * HD + i], oe[i]);
+        }
+        float *ph = part + ((size_t)h * gridDim.y + c) * (HD + 2);
+#pragma unroll
+        for (int i = 0; i < DPL; i++) ph[2 + DPL * lane + i] = oe[i] + oo[i];
+        if (lane == 0) {
+            ph[0] = m;
+            ph[1] = l;
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -348,13 +505,31 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
     const size_t lds = sizeof(float) * ((size_t)tc * (head_dim + 1) + (size_t)tc * head_dim +
                                         (size_t)nw * (head_dim + tc));
     static const bool attr = [] {
-        bool ok = hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_chunk_k<true>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
-        return ok && hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_chunk_k<false>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+        const void *fs[] = {reinterpret_cast<const void *>(&attn_chunk_k<true>),
+                            reinterpret_cast<const void *>(&attn_chunk_k<false>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<true, 64>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<false, 64>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<true, 128>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<false, 128>)};
+        bool ok = true;
+        for (const void *f : fs)
+            ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+        return ok;
     }();
     (void)attr;
-    if (fused)
+    if (head_dim == 64 || head_dim == 128) {
+        const size_t lds_hd = sizeof(float) * (2 * (size_t)tc * head_dim + head_dim + (size_t)nw * (head_dim + tc));
+#define JH_ATT(FU, HD)                                                                                       \
+    attn_chunk_hd<FU, HD><<<grid, 64 * nw, lds_hd, s>>>(q, FU ? k_new : nullptr, FU ? v_new : nullptr, k_cache,   \
+                                                       v_cache, n_heads, n_kv_heads, d_pos, max_seq, theta, scale, \
+                                                       part, d_slot, n_slots)
+        if (head_dim == 64) {
+            if (fused) JH_ATT(true, 64); else JH_ATT(false, 64);
+        } else {
+            if (fused) JH_ATT(true, 128); else JH_ATT(false, 128);
+        }
+#undef JH_ATT
+    } else if (fused)
         attn_chunk_k<true><<<grid, 64 * nw, lds, s>>>(q, k_new, v_new, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos,
                                                 max_seq, theta, scale, part, d_slot, n_slots);
     else
