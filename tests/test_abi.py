@@ -79,6 +79,23 @@ def test_null_matrix_is_illegal_argument():
         mv._check(rc)
 
 
+def test_batched_group_argument_checks_without_gpu():
+    """jh_qmatvec_batched_group_dev rejects a bad group before any device call:
+    more than 4 matrices, negative B, null arrays or a null matrix; n = 0 and
+    B = 0 are no-ops."""
+    L = _lib.load()
+    V = ctypes.c_void_p
+    arr = (V * 5)()
+    assert L.jh_qmatvec_batched_group_dev(5, arr, arr, 32, arr, None) == _lib.JH_EINVAL
+    assert "outside [0, 4]" in _lib.last_error()
+    assert L.jh_qmatvec_batched_group_dev(1, arr, arr, -1, arr, None) == _lib.JH_EINVAL
+    assert L.jh_qmatvec_batched_group_dev(1, None, arr, 32, arr, None) == _lib.JH_EINVAL
+    assert L.jh_qmatvec_batched_group_dev(1, arr, arr, 32, arr, None) == _lib.JH_EINVAL  # null matrix
+    assert "must not be null" in _lib.last_error()
+    assert L.jh_qmatvec_batched_group_dev(0, None, None, 32, None, None) == _lib.JH_OK
+    assert L.jh_qmatvec_batched_group_dev(1, arr, arr, 0, arr, None) == _lib.JH_OK
+
+
 def test_oracle_is_not_imported_by_the_product():
     for dirpath, _, files in os.walk(os.path.join(ROOT, "juno_amd")):
         for f in files:
