@@ -37,8 +37,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
-Q4_K, Q6_K = 12, 14
-BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210)}
+Q8_0, Q4_K, Q6_K = 8, 12, 14
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+PEAK_MFMA_F16_TFLOPS = 2500.0  # dense fp16 MFMA
 
 HIDDEN, FFN, KV, VOCAB, LAYERS = 4096, 14336, 1024, 128256, 32
 # (name, rows, cols, type)
@@ -240,6 +241,78 @@ def cpu_baseline(torch, mats, budget_s):
 def step_bytes(B):
     tot = sum(algo_bytes(r, c, t, B) for _, r, c, t in LAYER) * LAYERS
     return tot + algo_bytes(HEAD[1], HEAD[2], HEAD[3], B)
+
+
+def step_flops(B):
+    """Algorithmic GEMV flops of one 8B step at batch B: 2 B rows cols per GEMV."""
+    return 2 * B * (sum(r * c for _, r, c, _ in LAYER) * LAYERS + HEAD[1] * HEAD[2])
+
+
+def batch_sweep(torch, L, mats, stream, steps):
+    """the 8B GEMV step at B in {8, 16, 32, 64} (grouped like
+    B = 1; fp16 MFMA from B = 3).  MFMA utilisation = algorithmic flops over the
+    dense fp16 peak; the kernels issue twice that (x as hi + lo fp16 limbs)."""
+    out = {}
+    for B in (8, 16, 32, 64):
+        launch, _ = make_step(torch, L, mats, B, stream)
+        ms, _ = time_graph(torch, launch, stream, steps, 2)
+        tf = step_flops(B) / (ms * 1e-3) / 1e12
+        out[f"b{B}"] = {"ms_per_step": round(ms, 4), "tok_s": round(B * 1e3 / ms, 1),
+                        "GB_s": round(step_bytes(B) / (ms * 1e-3) / 1e9, 1), "algorithmic_TFLOP_s": round(tf, 1),
+                        "mfma_util": round(tf / PEAK_MFMA_F16_TFLOPS, 4) if B >= 3 else None,
+                        "mfma_issued_util": round(2 * tf / PEAK_MFMA_F16_TFLOPS, 4) if B >= 3 else None}
+    return out
+
+
+def rotated_gemv(torch, be, L, stream, qtype, rows, cols, B, seed, outliers=False, min_bytes=512 << 20, reps=5):
+    """One GEMV shape timed over enough packed copies (>= min_bytes in all) that
+    no launch finds its weights in the 256 MB memory-side cache; returns
+    (us per GEMV, algorithmic GB/s)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    one = packed_bytes(rows, cols, qtype)
+    n = max(2, -(-min_bytes // one))
+    w = torch.randn(rows * cols, generator=g, device="cuda").mul_(0.02)
+    if outliers:  # 1 % of the entries at 10x (seeded choice)
+        idx = torch.randperm(rows * cols, generator=g, device="cuda")[: rows * cols // 100]
+        w[idx] *= 10
+    cur = torch.cuda.current_stream().cuda_stream
+    mats = [be.quantize_dev(qtype, w.data_ptr(), rows, cols, cur) for _ in range(n)]
+    del w
+    x = torch.randn(B, cols, generator=g, device="cuda")
+    y = torch.empty(B, rows, device="cuda")
+    s = ctypes.c_void_p(stream.cuda_stream)
+    torch.cuda.synchronize()
+
+    def launch():
+        for m in mats:
+            if L.jh_qmatvec_batched_dev(m.handle, ctypes.c_void_p(x.data_ptr()), B, ctypes.c_void_p(y.data_ptr()), 0,
+                                        rows, s):
+                raise RuntimeError(L.jh_last_error().decode())
+    ms, _ = time_graph(torch, launch, stream, reps, 1)
+    for m in mats:
+        m.close()
+    torch.cuda.synchronize()
+    us = ms * 1e3 / n
+    return us, algo_bytes(rows, cols, qtype, B) / (us * 1e-6) / 1e9
+
+
+def shape_sweeps(torch, be, L, stream):
+    """BASELINE config 1 (single Q4_K GEMV at the TinyLlama up-projection shape)
+    and config 5 (Phi-3-mini-shaped Q8_0 and Q6_K GEMVs with 1 % outliers at 10x,
+    B = 1 and 32), each over rotated copies."""
+    us, gbs = rotated_gemv(torch, be, L, stream, Q4_K, 5632, 2048, 1, 21)
+    cfg1 = {"shape": "5632x2048", "type": "Q4_K", "batch": 1, "us": round(us, 2), "GB_s": round(gbs, 1),
+            "pct_of_peak": round(100 * gbs / PEAK_HBM_GBS, 2)}
+    phi = {}
+    shapes = {"qkv": (9216, 3072), "o": (3072, 3072), "gate_up": (16384, 3072), "down": (3072, 8192),
+              "lm_head": (32064, 3072)}
+    for qt, tn in ((Q8_0, "Q8_0"), (Q6_K, "Q6_K")):
+        for name, (r, c) in shapes.items():
+            for B in (1, 32):
+                us, gbs = rotated_gemv(torch, be, L, stream, qt, r, c, B, 30 + r + c + B, outliers=True)
+                phi[f"{tn}.{name}.b{B}"] = {"us": round(us, 2), "GB_s": round(gbs, 1)}
+    return {"config1_tinyllama_up_q4k": cfg1, "config5_phi3": phi}
 
 
 def parity_spot_check(torch, L, mats, stream):
@@ -490,6 +563,13 @@ def main():
                    "GB_s": round(sb32 / (ms32 * 1e-3) / 1e9, 1)}
         log(f"B=32 step: {ms32:.4f} ms  {batched}")
 
+    sweep = None
+    if not args.no_batched:
+        sweep = batch_sweep(torch, L, mats, stream, max(args.steps // 5, 3))
+        log(f"batched sweep: {sweep}")
+    shapes = shape_sweeps(torch, be, L, stream)
+    log(f"shape sweeps: {shapes}")
+
     full8b = {"b1": decode_step_8b(torch, be, stream, max(args.steps // 2, 10), mats, 1)}
     log(f"8B full decode step, B=1: {full8b['b1']}")
     if not args.no_batched:
@@ -534,6 +614,8 @@ def main():
                      "algorithmic_bytes_per_launch": per_launch},
         "cpu_baseline": cpu,
         "batched": batched,
+        "batched_sweep": sweep,
+        "shape_sweeps": shapes,
         "decode_step_8b": full8b,
         "decode_step_tinyllama": tiny,
         "parity_max_rel_err": parity,

@@ -149,7 +149,7 @@ int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *
                          void *stream);
 
 /* Batched form of jh_qmatvec_group_dev: Y_i[B][rows_i] = X_i[B][cols] W_i^T
- * for n <= 4 matrices, full row ranges, one launch when B >= 16 and the
+ * for n <= 4 matrices, full row ranges, one launch when B >= 3 and the
  * matrices share cols (the MFMA path; formats may differ, e.g. the Q4_K q / k
  * and Q6_K v of a Q4_K_M layer), else one call per matrix.  Same results as
  * n calls of jh_qmatvec_batched_dev.  The reference's forwardBatch runs the

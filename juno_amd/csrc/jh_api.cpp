@@ -230,7 +230,7 @@ int stream_workspace(int device, hipStream_t s, size_t bytes, void **out) {
     return JH_OK;
 }
 
-// The MFMA path for a group of matrices sharing K (B >= 16): kMfmaNotApplicable
+// The MFMA path for a group of matrices sharing K (B >= kMfmaMinBatch): kMfmaNotApplicable
 // (never returned through the C ABI) when it does not apply, so that the caller
 // can take the per-matrix kernels.
 constexpr int kMfmaNotApplicable = -1;
@@ -250,7 +250,7 @@ int enqueue_mfma_group(int device, int n, const jh::MfmaDesc *d, int B, hipStrea
 }
 
 // Enqueue y = W x for B vectors (device pointers), splitting B into the
-// kernel's supported batch widths, or using the MFMA path for B >= 16.
+// kernel's supported batch widths, or using the MFMA path for B >= kMfmaMinBatch.
 int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int row_start, int row_end,
                    hipStream_t s) {
     const int nrows = row_end - row_start;
@@ -264,7 +264,7 @@ int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int ro
     a.row_end = row_end;
     a.ldx = m->cols;
     a.ldy = nrows;
-    if (B >= 16) {
+    if (B >= jh::kMfmaMinBatch) {
         const jh::MfmaDesc d{m->type, m->d_raw, m->pitch, m->cols, row_start, row_end, d_x, d_y};
         int rc = enqueue_mfma_group(m->ctx->device, 1, &d, B, s);
         if (rc != kMfmaNotApplicable) return rc;
@@ -614,7 +614,7 @@ int jh_qmatvec_batched_group_dev(int n, const jh_qmat *const *mats, const float 
         d[i] = jh::MfmaDesc{mats[i]->type, mats[i]->d_raw, mats[i]->pitch, mats[i]->cols, 0, mats[i]->rows, d_X[i], d_Y[i]};
     }
     hipStream_t s = (hipStream_t)stream;
-    if (B >= 16) {
+    if (B >= jh::kMfmaMinBatch) {
         rc = enqueue_mfma_group(mats[0]->ctx->device, n, d, B, s);
         if (rc != kMfmaNotApplicable) return rc ? rc : ok();
     }

@@ -55,8 +55,8 @@ hipError_t launch_gemv_staged_group(int n, const GroupProblem *p, hipStream_t s)
 bool staged_supported(int type, int cols);
 hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s);
 
-// Batched decode through the LDS-staged, fp16-MFMA path (16 <= B <= 64).
-// Batched GEMVs (16 <= B <= 64) on fp16 MFMA: up to kMaxMfmaGroup matrices
+// Batched decode through the LDS-staged, fp16-MFMA path (kMfmaMinBatch <= B <= 64).
+// Batched GEMVs (kMfmaMinBatch <= B <= 64) on fp16 MFMA: up to kMaxMfmaGroup matrices
 // with the same cols, each with its own x [B][cols] and y [B][row_end -
 // row_start], in one launch.  mfma_group_workspace_bytes returns 0 when the
 // path does not apply (types, shapes, alignment); otherwise launch_mfma_group
@@ -72,6 +72,10 @@ struct MfmaDesc {
     float *y;
 };
 constexpr int kMaxMfmaGroup = 4;
+// Smallest batch that takes the MFMA path.  The x tile is padded to 32 columns, so a launch costs about the same from
+// B = 3 to 32.  Measured 8B GEMV step: B = 2 3.24 ms (VALU kernels) vs 3.78 ms (MFMA); B = 3 5.54 vs 3.80 ms; B = 8
+// 15.4 vs 3.88 ms.
+constexpr int kMfmaMinBatch = 3;
 size_t mfma_group_workspace_bytes(int n, const MfmaDesc *d, int B);
 hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, int *counters, hipStream_t s);
 

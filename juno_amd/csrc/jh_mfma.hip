@@ -1,4 +1,4 @@
-// jh_mfma.hip -- batched decode (16 <= B <= 64) on Q4_K / Q5_K / Q6_K / Q8_0 through
+// jh_mfma.hip -- batched decode (3 <= B <= 64) on Q4_K / Q5_K / Q6_K / Q8_0 through
 // LDS + fp16 MFMA.
 //
 // Y[b][r] = sum_c deq(W[r][c]) * X[b][c] is a dense contraction once B >= 16:
@@ -886,7 +886,7 @@ __global__ __launch_bounds__(kThreads) void mfma_px(const uint8_t *__restrict__ 
 
 // ------------------------------------------------------------------ host side
 static bool mfma_applies(const MfmaDesc &d, int B) {
-    if ((d.type != 12 && d.type != 13 && d.type != 14 && d.type != 8) || B < 16 || B > 64 || d.cols % 256 ||
+    if ((d.type != 12 && d.type != 13 && d.type != 14 && d.type != 8) || B < kMfmaMinBatch || B > 64 || d.cols % 256 ||
         d.cols <= 0 || d.row_end <= d.row_start)
         return false;
     if ((d.type == 12 || d.type == 13) && ((reinterpret_cast<uintptr_t>(d.w) | d.pitch) & 15))

@@ -315,7 +315,7 @@ class HipMatVec:
 
     def sgemv_batched_group_dev(self, mats, d_Xs, B: int, d_Ys, stream: int = 0) -> None:
         """Y_i [B][rows_i] = X_i [B][cols] W_i^T for up to 4 matrices sharing cols:
-        one launch on the MFMA path (B >= 16), else one batched call per matrix."""
+        one launch on the MFMA path (B >= 3), else one batched call per matrix."""
         n = len(mats)
         if not (len(d_Xs) == len(d_Ys) == n):
             raise IllegalArgumentException("mats, X and Y must have the same length")

@@ -11,7 +11,7 @@ Mirrors the reference's pipeline contract (paths under
   InferencePipeline.forwardBatch (:47-69): the reference's default is a serial
   loop over forward(); here the N requests are stacked and every layer runs
   once for all of them (batched GEMVs, [q, k, v] and [gate, up] grouped: the
-  B <= 8 GEMV kernel, fp16 MFMA from B = 16, one launch per group; one batched
+  B <= 2 GEMV kernels, fp16 MFMA from B = 3, one launch per group; one batched
   rope + KV-append + attention launch pair)
 * ``vocab_size()``  InferencePipeline.vocabSize (:71-75)
 * ``evict(request_id)``  LlamaTransformerHandler.evict (:496-504)

@@ -5,7 +5,7 @@ attention over per-request cache slots) against N single-request decoders
 InferencePipeline.java:62-69) and against the oracle's transformerLayer.
 
 Tolerance: logits within 1e-3 of max|logit| (the batched kernels differ from
-the B = 1 kernels in the order of fp32 sums, and the MFMA path at B >= 16 in
+the B = 1 kernels in the order of fp32 sums, and the MFMA path at B >= 3 in
 x's hi/lo fp16 split, both inside the GEMV bar).
 """
 import numpy as np
