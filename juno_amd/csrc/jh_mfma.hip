@@ -58,7 +58,7 @@ constexpr int kXPad = 8;  // halves of padding per LDS column (spreads banks)
 // lo halves) and the super-block sum S are formed over 4-value groups with
 // fixed butterflies (deterministic).
 __device__ __forceinline__ void stage_x_column(const float (&xv)[16], int q, _Float16 *sh_hi, _Float16 *sh_lo,
-                                               _Float16 *sh_xs, float2 *sh_S, int col, int colh) {
+                                               _Float16 *sh_xs, _Float16 *sh_x16, float2 *sh_S, int col, int colh) {
     float m = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(xv[j]));
@@ -89,8 +89,14 @@ __device__ __forceinline__ void stage_x_column(const float (&xv)[16], int q, _Fl
         }
         g[k] = sum;
     }
-    // sub-block (32 values = groups 8i .. 8i+7 = this lane and its neighbour)
+    // 16-value group q (this lane's values): hi + lo in sh_x16 (the Q2_K min term)
     float sub = (g[0] + g[1]) + (g[2] + g[3]);
+    {
+        const _Float16 h = (_Float16)sub;
+        sh_x16[col * 32 + q] = h;
+        sh_x16[col * 32 + 16 + q] = (_Float16)(sub - (float)h);
+    }
+    // sub-block (32 values = groups 8i .. 8i+7 = this lane and its neighbour)
     sub += __shfl_xor(sub, 1);
     if ((q & 1) == 0) {
         const _Float16 h = (_Float16)sub;
@@ -123,8 +129,13 @@ constexpr int COLH = 256 + kXPad;  // halves per LDS column of the staged x slic
 // col at col * COLH halves (hi and lo), its sub-block sums at col * 16.
 struct Ctx {
     int wave, lr, kh;
-    const _Float16 *sh_hi, *sh_lo, *sh_xs;
+    const _Float16 *sh_hi, *sh_lo, *sh_xs, *sh_x16;
     const float2 *sh_S;
+    // 16-column group sums of x, K-half kh: hi limbs, then lo limbs
+    __device__ __forceinline__ half8 x16h(int col) const { return *reinterpret_cast<const half8 *>(sh_x16 + col * 32 + 8 * kh); }
+    __device__ __forceinline__ half8 x16l(int col) const {
+        return *reinterpret_cast<const half8 *>(sh_x16 + col * 32 + 16 + 8 * kh);
+    }
     __device__ __forceinline__ half8 xh(int col, int xoff) const {
         return *reinterpret_cast<const half8 *>(sh_hi + col * COLH + xoff);
     }
@@ -452,6 +463,129 @@ struct FmtQ8_0 {
     }
 };
 
+// Q2_K (matVecQ2Kraw, LlamaTransformerHandler.java): 84-byte blocks [scales 16]
+// [qs 64][d][dmin]; element 128h + 16k + l takes 2 bits at shift 2(k/2) of
+// qs[32h + 16(k&1) + l] and sub-block scale byte sc[8h + k] (low nibble scale,
+// high nibble min): w = d*(sc&15)*q - dmin*(sc>>4).  A 16-column sub-block is one
+// K-step t = 8h + k: B = q (exact), folded per K-step with d*(sc&15); the min
+// term is one MFMA pair per super-block against the 16-column sums of x.
+// Blocks are 4-byte aligned (84 = 4 * 21).
+struct FmtQ2K {
+    static constexpr int kBytes = 84;
+    static constexpr int kChunks = (kBytes + 12 + 15) / 16;  // a 4-byte-aligned block spans <= 6 chunks
+    static constexpr int kRowChunks = kChunks + 1;           // 28-dword window rows (2-way bank conflicts)
+    static constexpr bool kSums = false;
+    struct Regs {
+        u32x2 q[2][2];  // [h][k&1]: qs bytes 32h + 16(k&1) + 8kh .. +8
+        u32x4 sc;       // the 16 scale bytes
+        uint32_t dm;    // d (low half), dmin (high half)
+    };
+    template <bool RA>
+    static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int o = 0; o < 2; o++) r.q[h][o] = lds_u32x2(p + 16 + 32 * h + 16 * o + 8 * kh);
+        r.sc = lds_u32x4(p);
+        uint32_t dm[1];
+        lds_read_u<1>(p + 80, dm);
+        r.dm = dm[0];
+    }
+    template <int NT, class C>
+    static __device__ __forceinline__ void compute(const Regs &r, const C &c, f32x16 *tot) {
+        const half2v off = {(_Float16)1024.f, (_Float16)1024.f};
+        const float d = half_bits_to_float(r.dm), dmin = half_bits_to_float(r.dm >> 16);
+        auto scb = [&](int t) { return byte_of(t < 4 ? r.sc.x : t < 8 ? r.sc.y : t < 12 ? r.sc.z : r.sc.w, t & 3); };
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const int h = t >> 3, k = t & 7;
+            const u32x2 q = r.q[h][k & 1];
+            const uint32_t u0 = (q.x >> (2 * (k >> 1))) & 0x03030303u, u1 = (q.y >> (2 * (k >> 1))) & 0x03030303u;
+            f32x16 acc[NT];
+#pragma unroll
+            for (int m = 0; m < NT; m++) acc[m] = (f32x16){};
+            mfma_xw<NT>(c, bytes_to_h8(u0, u1, off), 16 * t + 8 * c.kh, acc);
+            const float ds = d * (float)(scb(t) & 15u);
+#pragma unroll
+            for (int m = 0; m < NT; m++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) tot[m][i] = fmaf(ds, acc[m][i], tot[m][i]);
+        }
+        // min term: sum_t (sc_t >> 4) * X16_t, K-half kh holding t = 8kh .. 8kh+7
+        half8 wm;
+#pragma unroll
+        for (int j = 0; j < 8; j++) wm[j] = (_Float16)(float)(scb(8 * c.kh + j) >> 4);
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+            const int col = n * 32 + c.lr;
+            f32x16 mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(c.x16h(col), wm, (f32x16){}, 0, 0, 0);
+            mn = __builtin_amdgcn_mfma_f32_32x32x16_f16(c.x16l(col), wm, mn, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 16; i++) tot[n][i] = fmaf(-dmin, mn[i], tot[n][i]);
+        }
+    }
+};
+
+// Q3_K (matVecQ3Kraw, LlamaTransformerHandler.java): 110-byte blocks [hmask 32]
+// [qs 64][scales 12][d]; sub-block t = 8h + 2j + r covers columns 128h + 32j +
+// 16r + l, whose 3-bit quant is 2 bits at shift 2j of qs[32h + 16r + l] and bit
+// 4h + j of hmask[16r + l], minus 4, with the 6-bit scale of t minus 32:
+// w = d*(sc - 32)*(q - 4).  B = q - 4 (exact), folded per K-step.  Blocks are
+// 2-byte aligned: fields are read as aligned dwords and realigned.
+struct FmtQ3K {
+    static constexpr int kBytes = 110;
+    static constexpr int kChunks = (kBytes + 14 + 15) / 16;  // a 2-byte-aligned block spans <= 8 chunks
+    static constexpr int kRowChunks = kChunks + 1;           // 36-dword window rows (2-way bank conflicts)
+    static constexpr bool kSums = false;
+    struct Regs {
+        u32x2 q[2][2];  // [h][r]: qs bytes 32 + 32h + 16r + 8kh .. +8
+        u32x2 hm[2];    // [r]: hmask bytes 16r + 8kh .. +8
+        u32x4 sd;       // scale bytes 96..107 (aux0, aux1, aux2), then d in the low half of .w
+    };
+    template <bool RA>
+    static __device__ __forceinline__ void load(Regs &r, const uint8_t *p, int kh) {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int o = 0; o < 2; o++) r.q[h][o] = lds_u32x2(p + 32 + 32 * h + 16 * o + 8 * kh);
+#pragma unroll
+        for (int o = 0; o < 2; o++) r.hm[o] = lds_u32x2(p + 16 * o + 8 * kh);
+        r.sd = lds_u32x4(p + 96);
+    }
+    template <int NT, class C>
+    static __device__ __forceinline__ void compute(const Regs &r, const C &c, f32x16 *tot) {
+        const half2v off = {(_Float16)1028.f, (_Float16)1028.f};  // 1024 + 4
+        const float d = half_bits_to_float(r.sd.w);
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            // the scale words of this half (utmp[2h], utmp[2h+1] of dequantizeQ3K)
+            const uint32_t aux2 = r.sd.z;
+            const uint32_t ua = ((r.sd.x >> (4 * h)) & 0x0f0f0f0fu) | (((aux2 >> (4 * h)) & 0x03030303u) << 4);
+            const uint32_t ub = ((r.sd.y >> (4 * h)) & 0x0f0f0f0fu) | (((aux2 >> (4 * h + 2)) & 0x03030303u) << 4);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int rr = 0; rr < 2; rr++) {
+                    const int t = 8 * h + 2 * j + rr;
+                    const u32x2 q = r.q[h][rr], hm = r.hm[rr];
+                    const int hb = 4 * h + j;
+                    const uint32_t u0 = ((q.x >> (2 * j)) & 0x03030303u) | (((hm.x >> hb) & 0x01010101u) << 2);
+                    const uint32_t u1 = ((q.y >> (2 * j)) & 0x03030303u) | (((hm.y >> hb) & 0x01010101u) << 2);
+                    f32x16 acc[NT];
+#pragma unroll
+                    for (int m = 0; m < NT; m++) acc[m] = (f32x16){};
+                    mfma_xw<NT>(c, bytes_to_h8(u0, u1, off), 16 * t + 8 * c.kh, acc);
+                    const int s6 = (int)byte_of(j < 2 ? ua : ub, 2 * (j & 1) + rr) - 32;
+                    const float ds = d * (float)s6;
+#pragma unroll
+                    for (int m = 0; m < NT; m++)
+#pragma unroll
+                        for (int i = 0; i < 16; i++) tot[m][i] = fmaf(ds, acc[m][i], tot[m][i]);
+                }
+        }
+    }
+};
+
 // ------------------------------------------------------------------ tile output
 // A workgroup's tile goes straight into y when K is not split.  Otherwise
 // each split stores its partial tile with coherent (L2-bypassing) stores and
@@ -560,7 +694,7 @@ struct MfmaGroup {
     int n, nsb, ksb, ksplit, B;
 };
 
-// format mask bits: Q4_K, Q5_K, Q6_K, Q8_0
+// format mask bits: Q4_K, Q5_K, Q6_K, Q8_0, Q2_K, Q3_K
 template <int MASK>
 __host__ __device__ constexpr int max_chunks() {
     int c = 0;
@@ -568,11 +702,14 @@ __host__ __device__ constexpr int max_chunks() {
     if (MASK & 2) c = c > FmtQ5K::kRowChunks ? c : FmtQ5K::kRowChunks;
     if (MASK & 4) c = c > FmtQ6K::kRowChunks ? c : FmtQ6K::kRowChunks;
     if (MASK & 8) c = c > FmtQ8_0::kRowChunks ? c : FmtQ8_0::kRowChunks;
+    if (MASK & 16) c = c > FmtQ2K::kRowChunks ? c : FmtQ2K::kRowChunks;
+    if (MASK & 32) c = c > FmtQ3K::kRowChunks ? c : FmtQ3K::kRowChunks;
     return c;
 }
-// LDS image: [x hi: BP x COLH][x lo: BP x COLH][sums: BP x 16 halves][(S, 1/s): BP][weight windows]
+// LDS image: [x hi: BP x COLH][x lo: BP x COLH][32-column sums: BP x 16 halves][16-column sums: BP x 32 halves]
+// [(S, 1/s): BP][weight windows]
 template <int NT>
-__host__ __device__ constexpr int lds_w_offset() { return (2 * 32 * NT * COLH + 32 * NT * 16) * 2 + 32 * NT * 8; }
+__host__ __device__ constexpr int lds_w_offset() { return (2 * 32 * NT * COLH + 32 * NT * 16 + 32 * NT * 32) * 2 + 32 * NT * 8; }
 template <int NT, int MASK>
 __host__ __device__ constexpr int lds_bytes() {
     return lds_w_offset<NT>() + kWaves * kRowsPerWave * max_chunks<MASK>() * 16 + kWinPad;
@@ -589,7 +726,8 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
     _Float16 *sh_hi = reinterpret_cast<_Float16 *>(lds);
     _Float16 *sh_lo = sh_hi + BP * COLH;
     _Float16 *sh_xs = sh_lo + BP * COLH;
-    float2 *sh_S = reinterpret_cast<float2 *>(sh_xs + BP * 16);  // (sum of x, 1 / column scale) per column
+    _Float16 *sh_x16 = sh_xs + BP * 16;
+    float2 *sh_S = reinterpret_cast<float2 *>(sh_x16 + BP * 32);  // (sum of x, 1 / column scale) per column
     const uint8_t *__restrict__ W = P.w;
     const float *__restrict__ X = P.x;
     const size_t pitch = P.pitch;
@@ -597,7 +735,7 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const Ctx c{wave, lane & 31, lane >> 5, sh_hi, sh_lo, sh_xs, sh_S};
+    const Ctx c{wave, lane & 31, lane >> 5, sh_hi, sh_lo, sh_xs, sh_x16, sh_S};
     const int rbase = tile * kRowsPerWG + wave * kRowsPerWave;
     const int sb0 = split * g.ksb, sb1 = min(g.nsb, sb0 + g.ksb);
     auto row_off = [&](int rho) { return (size_t)(row0 + min(rbase + rho, nrows - 1)) * pitch; };
@@ -650,7 +788,7 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
         __syncthreads();  // the previous super-block's LDS contents are consumed
 #pragma unroll
         for (int i = 0; i < CPT; i++)
-            stage_x_column(xv_n[i], xq, sh_hi, sh_lo, sh_xs, sh_S, xcol + 32 * i, COLH);
+            stage_x_column(xv_n[i], xq, sh_hi, sh_lo, sh_xs, sh_x16, sh_S, xcol + 32 * i, COLH);
 #pragma unroll
         for (int k = 0; k < CL; k++)
             if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot + 16 * win_chunk<CH, RC>(lane + 64 * k)) = ch_n[0][k];
@@ -704,6 +842,8 @@ __global__ __launch_bounds__(kThreads) void mfma_group(MfmaGroup g) {
         case 12: if constexpr ((MASK & 1) != 0) gemm_body<FmtQ4K, NT, PD>(P, tile, split, g, lds); break;
         case 13: if constexpr ((MASK & 2) != 0) gemm_body<FmtQ5K, NT, PD>(P, tile, split, g, lds); break;
         case 14: if constexpr ((MASK & 4) != 0) gemm_body<FmtQ6K, NT, PD>(P, tile, split, g, lds); break;
+        case 10: if constexpr ((MASK & 16) != 0) gemm_body<FmtQ2K, NT, PD>(P, tile, split, g, lds); break;
+        case 11: if constexpr ((MASK & 32) != 0) gemm_body<FmtQ3K, NT, PD>(P, tile, split, g, lds); break;
         default: if constexpr ((MASK & 8) != 0) gemm_body<FmtQ8_0, NT, PD>(P, tile, split, g, lds); break;
     }
 }
@@ -886,7 +1026,8 @@ __global__ __launch_bounds__(kThreads) void mfma_px(const uint8_t *__restrict__ 
 
 // ------------------------------------------------------------------ host side
 static bool mfma_applies(const MfmaDesc &d, int B) {
-    if ((d.type != 12 && d.type != 13 && d.type != 14 && d.type != 8) || B < kMfmaMinBatch || B > 64 || d.cols % 256 ||
+    if ((d.type != 12 && d.type != 13 && d.type != 14 && d.type != 8 && d.type != 10 && d.type != 11) ||
+        B < kMfmaMinBatch || B > 64 || d.cols % 256 ||
         d.cols <= 0 || d.row_end <= d.row_start)
         return false;
     if ((d.type == 12 || d.type == 13) && ((reinterpret_cast<uintptr_t>(d.w) | d.pitch) & 15))
@@ -920,7 +1061,7 @@ static bool plan_group(int n, const MfmaDesc *d, int B, Plan &p) {
     p.ksplit = (p.nsb + p.ksb - 1) / p.ksb;
     if (p.ksplit > 1 && tiles > kMaxTileCounters) return false;
     p.grid = tiles * p.ksplit;
-    p.prepared = n == 1 && p.ksplit == 1 && B <= 32;
+    p.prepared = n == 1 && p.ksplit == 1 && B <= 32 && d[0].type != 10 && d[0].type != 11;  // slabs carry no 16-column sums
     p.slab_bytes = p.prepared ? (size_t)p.nsb * kSlabBytes : 0;
     p.part_floats = p.ksplit > 1 ? (size_t)p.ksplit * B * rows : 0;
     return true;
@@ -940,7 +1081,9 @@ static void launch_group_nt(const MfmaGroup &g, int mask, int grid, hipStream_t 
         case 2: mfma_group<NT, 2><<<grid, kThreads, 0, s>>>(g); break;
         case 4: mfma_group<NT, 4><<<grid, kThreads, 0, s>>>(g); break;
         case 8: mfma_group<NT, 8><<<grid, kThreads, 0, s>>>(g); break;
-        default: mfma_group<NT, 15><<<grid, kThreads, 0, s>>>(g); break;
+        case 16: mfma_group<NT, 16><<<grid, kThreads, 0, s>>>(g); break;
+        case 32: mfma_group<NT, 32><<<grid, kThreads, 0, s>>>(g); break;
+        default: mfma_group<NT, 63><<<grid, kThreads, 0, s>>>(g); break;
     }
 }
 
@@ -987,7 +1130,7 @@ hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, i
         wg += q.tiles * p.ksplit;
         cnt += q.tiles;
         part += p.ksplit > 1 ? (size_t)p.ksplit * B * q.rows : 0;
-        mask |= q.type == 12 ? 1 : q.type == 13 ? 2 : q.type == 14 ? 4 : 8;
+        mask |= q.type == 12 ? 1 : q.type == 13 ? 2 : q.type == 14 ? 4 : q.type == 10 ? 16 : q.type == 11 ? 32 : 8;
     }
     if (B <= 32) launch_group_nt<1>(g, mask, p.grid, s);
     else launch_group_nt<2>(g, mask, p.grid, s);

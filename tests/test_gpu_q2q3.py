@@ -78,7 +78,7 @@ def test_gemv_vs_oracle(be, qtype, rows, cols):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-@pytest.mark.parametrize("B", [2, 5, 8, 16, 20])
+@pytest.mark.parametrize("B", [2, 3, 5, 8, 16, 20, 32, 48])
 def test_batched_vs_oracle(be, qtype, B):
     rows, cols = 257, 1024
     raw = random_blocks(qtype, rows, cols, 7 * B + qtype)
@@ -89,6 +89,49 @@ def test_batched_vs_oracle(be, qtype, B):
     for j in range(B):
         ref = O.matvec(qtype, raw, X[j], 0, rows, cols).astype(np.float64)
         assert rel_err(Y[j], ref, deq, X[j]).max() <= 1e-3, j
+
+
+@pytest.mark.parametrize("qtype", TYPES)
+def test_batched_mfma_split_shapes(be, qtype):
+    """The MFMA path (B >= 3) at shapes whose K is split across workgroups
+    (the in-kernel hand-off) and at a wide row, B in {3, 32, 64}."""
+    for rows, cols in ((1024, 4096), (512, 14336)):
+        raw = random_blocks(qtype, rows, cols, 11 + rows + qtype)
+        deq = O.dequantize(qtype, raw, rows, cols)
+        with be.upload_quant(qtype, rows, cols, raw) as m:
+            for B in (3, 32, 64):
+                X = np.random.default_rng(B + rows).standard_normal((B, cols)).astype(np.float32)
+                Y = be.sgemv_batched(m, X)
+                for j in (0, B - 1):
+                    ref = O.matvec(qtype, raw, X[j], 0, rows, cols).astype(np.float64)
+                    assert rel_err(Y[j], ref, deq, X[j]).max() <= 1e-3, (rows, B, j)
+
+
+def test_batched_group_all_formats(be):
+    """One MFMA launch over Q2_K, Q3_K, Q4_K and Q6_K matrices sharing cols."""
+    B, cols = 32, 1024
+    shapes = [(O.Q2_K, 300), (O.Q3_K, 257), (O.Q4_K, 128), (O.Q6_K, 200)]
+    Xs = np.random.default_rng(5).standard_normal((B, cols)).astype(np.float32)
+    dX = torch.from_numpy(Xs).cuda()
+    mats, raws, ys = [], [], []
+    try:
+        for i, (t, r) in enumerate(shapes):
+            raw = random_blocks(t, r, cols, 90 + i) if t in TYPES else O.quantize(t, (np.random.default_rng(
+                90 + i).standard_normal(r * cols) * 0.02).astype(np.float32))
+            raws.append(raw)
+            mats.append(be.upload_quant(t, r, cols, raw))
+            ys.append(torch.full((B, r), float("nan"), device="cuda"))
+        be.sgemv_batched_group_dev(mats, [dX.data_ptr()] * 4, B, [y.data_ptr() for y in ys])
+        torch.cuda.synchronize()
+        for (t, r), raw, y in zip(shapes, raws, ys):
+            Y = y.cpu().numpy()
+            deq = O.dequantize(t, raw, r, cols)
+            for j in (0, B - 1):
+                ref = O.matvec(t, raw, Xs[j], 0, r, cols).astype(np.float64)
+                assert rel_err(Y[j], ref, deq, Xs[j]).max() <= 1e-3, (t, j)
+    finally:
+        for m in mats:
+            m.close()
 
 
 def test_group_dev_mixed_formats(be):
