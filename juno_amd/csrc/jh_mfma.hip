@@ -1043,8 +1043,7 @@ struct Plan {
 };
 }  // namespace
 
-// Row tiles of 256 rows; K is split until the grid has kMinWorkgroups
-// workgroups (one per CU), with the same split for every matrix of the group.
+// Row tiles of 256 rows; K split the same way for every matrix of the group.
 static bool plan_group(int n, const MfmaDesc *d, int B, Plan &p) {
     if (n < 1 || n > kMaxMfmaGroup) return false;
     int tiles = 0;
@@ -1055,10 +1054,25 @@ static bool plan_group(int n, const MfmaDesc *d, int B, Plan &p) {
         rows += d[i].row_end - d[i].row_start;
     }
     p.nsb = d[0].cols / 256;
-    int ks = (kMinWorkgroups + tiles - 1) / tiles;
-    ks = ks < 1 ? 1 : ks > p.nsb ? p.nsb : ks;
-    p.ksb = (p.nsb + ks - 1) / ks;
-    p.ksplit = (p.nsb + p.ksb - 1) / p.ksb;
+    // One workgroup fits per CU (LDS, VGPRs), so the grid runs in rounds of
+    // kMinWorkgroups.  Cost of a split, in super-block steps: rounds x (super-
+    // blocks per workgroup + a workgroup's fixed prologue and epilogue, ~5
+    // steps), plus one for the hand-off when K is split; the smallest split
+    // wins ties.  Fitted to the 8B B = 32 shapes ([gate, up]: 2 splits 44 us,
+    // 3 splits 57 us, 16 splits 96 us).
+    int best = 1 << 30;
+    p.ksb = p.nsb;
+    p.ksplit = 1;
+    for (int ks = 1; ks <= p.nsb; ks++) {
+        const int ksb = (p.nsb + ks - 1) / ks, kse = (p.nsb + ksb - 1) / ksb;
+        const int rounds = (tiles * kse + kMinWorkgroups - 1) / kMinWorkgroups;
+        const int cost = rounds * (ksb + 5) + (kse > 1 ? 1 : 0);
+        if (cost < best) {
+            best = cost;
+            p.ksb = ksb;
+            p.ksplit = kse;
+        }
+    }
     if (p.ksplit > 1 && tiles > kMaxTileCounters) return false;
     p.grid = tiles * p.ksplit;
     p.prepared = n == 1 && p.ksplit == 1 && B <= 32 && d[0].type != 10 && d[0].type != 11;  // slabs carry no 16-column sums
