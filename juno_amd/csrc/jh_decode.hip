@@ -35,8 +35,23 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_k(const float *x, const 
     if (res) res += row;
     if (x_out) x_out += row;
     out += row;
+    // up to kKeep values per thread stay in registers across the reduction (rows
+    // up to 8192); wider rows re-read them
+    constexpr int kKeep = 8;
+    float keep[kKeep];
     float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += kNormThreads) {
+#pragma unroll
+    for (int k = 0; k < kKeep; k++) {
+        const int i = threadIdx.x + k * kNormThreads;
+        float v = 0.f;
+        if (i < n) {
+            v = res ? x[i] + res[i] : x[i];
+            if (x_out) x_out[i] = v;
+        }
+        keep[k] = v;
+        ss += v * v;
+    }
+    for (int i = threadIdx.x + kKeep * kNormThreads; i < n; i += kNormThreads) {
         const float v = res ? x[i] + res[i] : x[i];
         if (x_out) x_out[i] = v;
         ss += v * v;
@@ -48,7 +63,12 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_k(const float *x, const 
 #pragma unroll
     for (int k = 0; k < kNormThreads / 64; k++) tot += part[k];
     const float scale = 1.f / (float)sqrt((double)(tot / (float)n + eps));
-    for (int i = threadIdx.x; i < n; i += kNormThreads) {  // the same i as above: x_out[i] is this thread's
+#pragma unroll
+    for (int k = 0; k < kKeep; k++) {
+        const int i = threadIdx.x + k * kNormThreads;
+        if (i < n) out[i] = w[i] * keep[k] * scale;
+    }
+    for (int i = threadIdx.x + kKeep * kNormThreads; i < n; i += kNormThreads) {  // x_out[i] is this thread's
         const float v = x_out ? x_out[i] : (res ? x[i] + res[i] : x[i]);
         out[i] = w[i] * v * scale;
     }

@@ -1065,6 +1065,7 @@ static bool plan_group(int n, const MfmaDesc *d, int B, Plan &p) {
     p.ksplit = 1;
     for (int ks = 1; ks <= p.nsb; ks++) {
         const int ksb = (p.nsb + ks - 1) / ks, kse = (p.nsb + ksb - 1) / ksb;
+        if (kse > 1 && tiles > kMaxTileCounters) break;  // a split needs a counter per tile
         const int rounds = (tiles * kse + kMinWorkgroups - 1) / kMinWorkgroups;
         const int cost = rounds * (ksb + 5) + (kse > 1 ? 1 : 0);
         if (cost < best) {
@@ -1073,7 +1074,6 @@ static bool plan_group(int n, const MfmaDesc *d, int B, Plan &p) {
             p.ksplit = kse;
         }
     }
-    if (p.ksplit > 1 && tiles > kMaxTileCounters) return false;
     p.grid = tiles * p.ksplit;
     p.prepared = n == 1 && p.ksplit == 1 && B <= 32 && d[0].type != 10 && d[0].type != 11;  // slabs carry no 16-column sums
     p.slab_bytes = p.prepared ? (size_t)p.nsb * kSlabBytes : 0;
