@@ -264,7 +264,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_k(
 // reads its row 16 bytes at a time and the 16 lanes of an LDS pass hit distinct
 // banks; q . k runs in four accumulators.  For p . V each lane owns HD / 64
 // adjacent output dims and alternates two accumulators over positions.
-template <bool FUSED, int HD>
+template <bool FUSED, int HD, bool VG>  // VG: p . V reads V from the cache (global) instead of LDS
 __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
     const float *__restrict__ q, const float *__restrict__ k_new, const float *__restrict__ v_new,
     float *__restrict__ k_cache, float *__restrict__ v_cache, int n_heads, int n_kv_heads, const int *__restrict__ d_pos,
@@ -273,8 +273,8 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
     extern __shared__ float lds[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     float4 *sk4 = reinterpret_cast<float4 *>(lds);  // [tc][Q4] swizzled
-    float *sv = lds + tc * HD;                        // [tc][HD]
-    float *srope = sv + tc * HD;                      // [HD / 2] (cos, sin) of this request's position
+    float *sv = lds + tc * HD;                        // [tc][HD] (not with VG)
+    float *srope = sv + (VG ? 0 : tc * HD);           // [HD / 2] (cos, sin) of this request's position
     float *sq = srope + HD + wave * (HD + tc);        // this wave's [HD] q, then [tc] weights
     float *sp = sq + HD;
     const int z = blockIdx.z, kv_dim = n_kv_heads * HD;
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
             const int i = base + u * blockDim.x + threadIdx.x, t = i / Q4, j = i % Q4;
             const size_t o = (size_t)min(t0 + t, T - 1) * kv_dim + g * HD + 4 * j;
             kk[u] = *reinterpret_cast<const float4 *>(k_cache + o);
-            vv[u] = *reinterpret_cast<const float4 *>(v_cache + o);
+            if (!VG) vv[u] = *reinterpret_cast<const float4 *>(v_cache + o);
         }
         // rope's (cos, sin) for this position, once per workgroup, while the first loads are in flight
         // (rope_pair's arithmetic: the same values)
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
             const int i = base + u * blockDim.x + threadIdx.x, t = i / Q4, j = i % Q4;
             if (t >= nt || (has_pos && t0 + t == pos)) continue;
             sk4[t * Q4 + (j ^ (t & M))] = kk[u];
-            *reinterpret_cast<float4 *>(sv + t * HD + 4 * j) = vv[u];
+            if (!VG) *reinterpret_cast<float4 *>(sv + t * HD + 4 * j) = vv[u];
         }
     }
     if (has_pos) {
@@ -338,8 +338,8 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
         }
         for (int d = threadIdx.x; d < HD; d += blockDim.x) {
             const float v = v_new[g * HD + d];
-            sv[tp * HD + d] = v;
-            v_cache[(size_t)pos * kv_dim + g * HD + d] = v;
+            if (!VG) sv[tp * HD + d] = v;
+            v_cache[(size_t)pos * kv_dim + g * HD + d] = v;  // VG: read back below, after the barrier
         }
     }
     __syncthreads();
@@ -379,20 +379,22 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
         float oe[DPL], oo[DPL];
 #pragma unroll
         for (int i = 0; i < DPL; i++) oe[i] = oo[i] = 0.f;
-        const float *vcol = sv + DPL * lane;
+        // V rows: LDS, or the cache rows t0 .. of head g (lanes read adjacent dims: coalesced)
+        const float *vcol = VG ? v_cache + (size_t)t0 * kv_dim + g * HD + DPL * lane : sv + DPL * lane;
+        const int vst = VG ? kv_dim : HD;
         int t = 0;
         for (; t + 1 < nt; t += 2) {
             const float pe = sp[t], po = sp[t + 1];
 #pragma unroll
             for (int i = 0; i < DPL; i++) {
-                oe[i] = fmaf(pe, vcol[t * HD + i], oe[i]);
-                oo[i] = fmaf(po, vcol[(t + 1) * HD + i], oo[i]);
+                oe[i] = fmaf(pe, vcol[(size_t)t * vst + i], oe[i]);
+                oo[i] = fmaf(po, vcol[(size_t)(t + 1) * vst + i], oo[i]);
             }
         }
         if (t < nt) {
             const float pe = sp[t];
 #pragma unroll
-            for (int i = 0; i < DPL; i++) oe[i] = fmaf(pe, vcol[t * HD + i], oe[i]);
+            for (int i = 0; i < DPL; i++) oe[i] = fmaf(pe, vcol[(size_t)t * vst + i], oe[i]);
         }
         float *ph = part + ((size_t)h * gridDim.y + c) * (HD + 2);
 #pragma unroll
@@ -507,6 +509,10 @@ hipError_t launch_rope_kv(float *q, const float *k, const float *v, int n_heads,
     return hipGetLastError();
 }
 
+// V read from the cache instead of LDS: measured at position 511, head_dim 128
+// B = 32 48.2 -> 45.3 us; slower for head_dim 64 (20.6 -> 29.5 us) and at B = 1
+static bool attn_v_global(int head_dim, int batch) { return head_dim == 128 && batch >= 8; }
+
 size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq, int batch) {
     const int nch = (max_seq + attn_tc(head_dim) - 1) / attn_tc(head_dim);
     return (size_t)batch * n_heads * nch * (head_dim + 2) * sizeof(float);
@@ -527,10 +533,14 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
     static const bool attr = [] {
         const void *fs[] = {reinterpret_cast<const void *>(&attn_chunk_k<true>),
                             reinterpret_cast<const void *>(&attn_chunk_k<false>),
-                            reinterpret_cast<const void *>(&attn_chunk_hd<true, 64>),
-                            reinterpret_cast<const void *>(&attn_chunk_hd<false, 64>),
-                            reinterpret_cast<const void *>(&attn_chunk_hd<true, 128>),
-                            reinterpret_cast<const void *>(&attn_chunk_hd<false, 128>)};
+                            reinterpret_cast<const void *>(&attn_chunk_hd<true, 64, false>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<false, 64, false>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<true, 128, false>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<false, 128, false>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<true, 64, true>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<false, 64, true>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<true, 128, true>),
+                            reinterpret_cast<const void *>(&attn_chunk_hd<false, 128, true>)};
         bool ok = true;
         for (const void *f : fs)
             ok = ok && hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
@@ -538,15 +548,27 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
     }();
     (void)attr;
     if (head_dim == 64 || head_dim == 128) {
-        const size_t lds_hd = sizeof(float) * (2 * (size_t)tc * head_dim + head_dim + (size_t)nw * (head_dim + tc));
-#define JH_ATT(FU, HD)                                                                                       \
-    attn_chunk_hd<FU, HD><<<grid, 64 * nw, lds_hd, s>>>(q, FU ? k_new : nullptr, FU ? v_new : nullptr, k_cache,   \
-                                                       v_cache, n_heads, n_kv_heads, d_pos, max_seq, theta, scale, \
-                                                       part, d_slot, n_slots)
+        // many workgroups (a batch): V is read from the cache, so that a workgroup's LDS holds only K and more of
+        // them fit per CU
+        const bool vg = attn_v_global(head_dim, batch);
+        const size_t lds_hd =
+            sizeof(float) * ((vg ? 1 : 2) * (size_t)tc * head_dim + head_dim + (size_t)nw * (head_dim + tc));
+#define JH_ATT(FU, HD, VG)                                                                                    \
+    attn_chunk_hd<FU, HD, VG><<<grid, 64 * nw, lds_hd, s>>>(q, FU ? k_new : nullptr, FU ? v_new : nullptr, k_cache,   \
+                                                           v_cache, n_heads, n_kv_heads, d_pos, max_seq, theta, scale, \
+                                                           part, d_slot, n_slots)
         if (head_dim == 64) {
-            if (fused) JH_ATT(true, 64); else JH_ATT(false, 64);
+            if (vg) {
+                if (fused) JH_ATT(true, 64, true); else JH_ATT(false, 64, true);
+            } else {
+                if (fused) JH_ATT(true, 64, false); else JH_ATT(false, 64, false);
+            }
         } else {
-            if (fused) JH_ATT(true, 128); else JH_ATT(false, 128);
+            if (vg) {
+                if (fused) JH_ATT(true, 128, true); else JH_ATT(false, 128, true);
+            } else {
+                if (fused) JH_ATT(true, 128, false); else JH_ATT(false, 128, false);
+            }
         }
 #undef JH_ATT
     } else if (fused)

@@ -136,6 +136,39 @@ def test_rope_attention_fused(L, nh, nkv, hd, pos):
     assert np.array_equal(dq.cpu().numpy(), q)  # q itself is not modified
 
 
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 4, 64), (32, 8, 128)])
+@pytest.mark.parametrize("batch", [2, 8, 12])
+def test_rope_attention_batched(L, nh, nkv, hd, batch):
+    """jh_rope_attention_batched_dev: each request at its own position and cache
+    slot (slots permuted) == the oracle's rope + append + gqa per request.
+    Batches of 8 and more at head_dim 128 read V from the cache instead of LDS."""
+    say("rope_attention_batched", nh, nkv, hd, batch)
+    max_seq, theta, kvd, n_slots = 300, 500000.0, nkv * hd, batch + 3
+    rng = np.random.default_rng(batch * 7 + hd)
+    pos = rng.integers(0, max_seq, batch)
+    pos[0], pos[-1] = 0, max_seq - 1
+    slots = rng.permutation(n_slots)[:batch]
+    q = vec(batch * nh * hd, 11 + batch).reshape(batch, nh * hd)
+    k = vec(batch * kvd, 12 + batch).reshape(batch, kvd)
+    v = vec(batch * kvd, 13 + batch).reshape(batch, kvd)
+    kc = vec(n_slots * max_seq * kvd, 14 + batch).reshape(n_slots, max_seq, kvd)
+    vc = vec(n_slots * max_seq * kvd, 15 + batch).reshape(n_slots, max_seq, kvd)
+    dkc, dvc = dev(kc), dev(vc)
+    out = torch.full((batch, nh * hd), float("nan"), device="cuda")
+    dpos, dslot = dev(pos, torch.int32), dev(slots, torch.int32)
+    assert L.jh_rope_attention_batched_dev(P(dev(q)), P(dev(k)), P(dev(v)), batch, nh, nkv, hd, P(dpos), P(dslot),
+                                           n_slots, max_seq, theta, P(dkc), P(dvc), P(out), None) == 0
+    got = out.cpu().numpy()
+    for z in range(batch):
+        p, sl = int(pos[z]), int(slots[z])
+        kc_ref, vc_ref = kc[sl].copy(), vc[sl].copy()
+        kc_ref[p] = O.rope(k[z], p, nkv, hd, theta)
+        vc_ref[p] = v[z]
+        ref = O.gqa(O.rope(q[z], p, nh, hd, theta), kc_ref, vc_ref, nh, nkv, hd, p + 1)
+        assert np.abs(got[z] - ref).max() <= 1e-5 * np.abs(ref).max() + 1e-7, z
+        assert np.array_equal(dvc[sl, p].cpu().numpy(), v[z])
+
+
 def test_attention_arguments(L):
     d = torch.zeros(64, device="cuda")
     pos = torch.zeros(1, dtype=torch.int32, device="cuda")
