@@ -383,6 +383,22 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
         const float *vcol = VG ? v_cache + (size_t)t0 * kv_dim + g * HD + DPL * lane : sv + DPL * lane;
         const int vst = VG ? kv_dim : HD;
         int t = 0;
+        if (VG) {  // eight rows' loads in flight before their FMAs (global latency)
+            for (; t + 7 < nt; t += 8) {
+                float vv[8][DPL];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+#pragma unroll
+                    for (int i = 0; i < DPL; i++) vv[u][i] = vcol[(size_t)(t + u) * vst + i];
+#pragma unroll
+                for (int u = 0; u < 8; u += 2)
+#pragma unroll
+                    for (int i = 0; i < DPL; i++) {
+                        oe[i] = fmaf(sp[t + u], vv[u][i], oe[i]);
+                        oo[i] = fmaf(sp[t + u + 1], vv[u + 1][i], oo[i]);
+                    }
+            }
+        }
         for (; t + 1 < nt; t += 2) {
             const float pe = sp[t], po = sp[t + 1];
 #pragma unroll
