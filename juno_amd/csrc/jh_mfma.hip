@@ -51,6 +51,27 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kRowsPerWG = kWaves * kRowsPerWave;
 constexpr int kXPad = 8;  // halves of padding per LDS column (spreads banks)
 
+// Reductions over the 16 lanes of one DPP row (lanes 16 r .. 16 r + 15): xor-1
+// and xor-2 butterflies, then the half-row and row mirrors.  Each step adds two
+// values that are equal across the lanes being paired, so every lane ends with
+// the bit-identical result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm 1,0,3,2
+    v += dpp_f<0x4E>(v);   // quad_perm 2,3,0,1
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    return v + dpp_f<0x140>(v);  // row_mirror
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    return fmaxf(v, dpp_f<0x140>(v));
+}
+
 // x into the LDS image of one column and super-block, inside the GEMM: 16
 // consecutive lanes hold its 256 values, 16 each (xv).  A power-of-two scale
 // puts max |x s| in [2^12, 2^13) (exact, undone on the partial sums), then x s
@@ -62,8 +83,7 @@ __device__ __forceinline__ void stage_x_column(const float (&xv)[16], int q, _Fl
     float m = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(xv[j]));
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));  // the 16 lanes of the column
+    m = row16_max(m);  // the 16 lanes of the column
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);
     const float s = m > 0.f ? ldexpf(1.f, 13 - e) : 1.f;
@@ -97,19 +117,14 @@ __device__ __forceinline__ void stage_x_column(const float (&xv)[16], int q, _Fl
         sh_x16[col * 32 + 16 + q] = (_Float16)(sub - (float)h);
     }
     // sub-block (32 values = groups 8i .. 8i+7 = this lane and its neighbour)
-    sub += __shfl_xor(sub, 1);
+    sub += dpp_f<0xB1>(sub);
     if ((q & 1) == 0) {
         const _Float16 h = (_Float16)sub;
         sh_xs[col * 16 + (q >> 1)] = h;
         sh_xs[col * 16 + 8 + (q >> 1)] = (_Float16)(sub - (float)h);
     }
-    // super-block total: a butterfly over the column's 64 groups (across the
-    // 16 lanes, then within the lane)
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) g[k] += __shfl_xor(g[k], o);
-    const float tot = (g[0] + g[2]) + (g[1] + g[3]);
+    // super-block total: the lane's 4 groups, then across the column's 16 lanes
+    const float tot = row16_sum((g[0] + g[2]) + (g[1] + g[3]));
     if (q == 0) sh_S[col] = make_float2(tot, 1.f / s);
 }
 
@@ -856,8 +871,7 @@ __device__ __forceinline__ void prep_x_column(const float (&xv)[16], int q, uint
     float m = 0.f;
 #pragma unroll
     for (int j = 0; j < 16; j++) m = fmaxf(m, fabsf(xv[j]));
-#pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = row16_max(m);
     int e = 0;
     if (m > 0.f) (void)frexpf(m, &e);
     const float s = m > 0.f ? ldexpf(1.f, 13 - e) : 1.f;
@@ -884,18 +898,14 @@ __device__ __forceinline__ void prep_x_column(const float (&xv)[16], int q, uint
         *reinterpret_cast<half8 *>(slab + kSlabLo + 16 * slot) = l[i];
     }
     float sub = (g[0] + g[1]) + (g[2] + g[3]);
-    sub += __shfl_xor(sub, 1);
+    sub += dpp_f<0xB1>(sub);
     if ((q & 1) == 0) {
         _Float16 *xs = reinterpret_cast<_Float16 *>(slab + kSlabXs) + col * 16;
         const _Float16 hs = (_Float16)sub;
         xs[q >> 1] = hs;
         xs[8 + (q >> 1)] = (_Float16)(sub - (float)hs);
     }
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) g[k] += __shfl_xor(g[k], o);
-    const float tot = (g[0] + g[2]) + (g[1] + g[3]);
+    const float tot = row16_sum((g[0] + g[2]) + (g[1] + g[3]));
     if (q == 0) reinterpret_cast<float2 *>(slab + kSlabS)[col] = make_float2(tot, 1.f / s);
 }
 
