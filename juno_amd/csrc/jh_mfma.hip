@@ -727,7 +727,7 @@ template <int NT>
 __host__ __device__ constexpr int lds_w_offset() { return (2 * 32 * NT * COLH + 32 * NT * 16 + 32 * NT * 32) * 2 + 32 * NT * 8; }
 template <int NT, int MASK>
 __host__ __device__ constexpr int lds_bytes() {
-    return lds_w_offset<NT>() + kWaves * kRowsPerWave * max_chunks<MASK>() * 16 + kWinPad;
+    return (NT == 1 ? 2 : 1) * lds_w_offset<NT>() + kWaves * kRowsPerWave * max_chunks<MASK>() * 16 + kWinPad;
 }
 
 // One workgroup's tile (32 rows per wave x all batch columns) over the K
@@ -795,6 +795,64 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
 #pragma unroll
     for (int n = 0; n < NT; n++) tot[n] = (f32x16){};
 
+    auto fold = [&](const typename F::Regs &w, const Ctx &cx) {
+        if constexpr (F::kSums) {
+            F::template compute<NT>(w, cx, tot);
+        } else {
+            f32x16 part[NT];
+#pragma unroll
+            for (int n = 0; n < NT; n++) part[n] = (f32x16){};
+            F::template compute<NT>(w, cx, part);
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+                float S[16], cs[16];
+                col_terms<NT>(cx, n, S, cs);
+#pragma unroll
+                for (int i = 0; i < 16; i++) tot[n][i] = fmaf(cs[i], part[n][i], tot[n][i]);
+            }
+        }
+    };
+
+    if constexpr (NT == 1 && PD == 1) {
+        // Two x buffers: super-block sb + 1's x is converted into the free
+        // buffer while sb's MFMAs run, with one barrier per super-block.  The
+        // buffer a step writes was last read by the previous step's MFMAs,
+        // which every wave finished before this step's barrier.
+        constexpr int XS = lds_w_offset<1>();  // bytes of one x buffer
+        auto ctx_at = [&](int buf) {
+            _Float16 *hi = reinterpret_cast<_Float16 *>(lds + buf * XS);
+            _Float16 *lo = hi + BP * COLH, *xs = lo + BP * COLH, *x16 = xs + BP * 16;
+            return Ctx{wave, lane & 31, lane >> 5, hi, lo, xs, x16, reinterpret_cast<float2 *>(x16 + BP * 32)};
+        };
+        auto stage_into = [&](int buf) {
+            const Ctx cx = ctx_at(buf);
+            stage_x_column(xv_n[0], xq, const_cast<_Float16 *>(cx.sh_hi), const_cast<_Float16 *>(cx.sh_lo),
+                           const_cast<_Float16 *>(cx.sh_xs), const_cast<_Float16 *>(cx.sh_x16),
+                           const_cast<float2 *>(cx.sh_S), xcol, COLH);
+        };
+        uint8_t *wslot2 = lds + 2 * XS + wave * (kRowsPerWave * RC * 16);
+        if (sb0 < sb1) {
+            JH_LOAD_X(sb0);
+            JH_LOAD_W(0, sb0);
+            stage_into(0);
+            if (sb0 + 1 < sb1) JH_LOAD_X(sb0 + 1);
+        }
+        for (int sb = sb0; sb < sb1; sb++) {
+            const int buf = (sb - sb0) & 1;
+            __syncthreads();  // x of sb is staged; the other buffer is free
+#pragma unroll
+            for (int k = 0; k < CL; k++)
+                if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot2 + 16 * win_chunk<CH, RC>(lane + 64 * k)) = ch_n[0][k];
+            typename F::Regs w;
+            F::template load<true>(w, wslot2 + c.lr * RC * 16 + ((myoff + (size_t)sb * F::kBytes) & 15), c.kh);
+            if (sb + 1 < sb1) {
+                stage_into(buf ^ 1);
+                if (sb + 2 < sb1) JH_LOAD_X(sb + 2);
+                JH_LOAD_W(0, sb + 1);
+            }
+            fold(w, ctx_at(buf));
+        }
+    } else {
     if (sb0 < sb1) JH_LOAD_X(sb0);
 #pragma unroll
     for (int st = 0; st < PD; st++)
@@ -818,21 +876,8 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
             for (int k = 0; k < CL; k++) ch_n[st][k] = ch_n[st + 1][k];
         if (sb + PD < sb1) JH_LOAD_W(PD - 1, sb + PD);
         __syncthreads();
-        if constexpr (F::kSums) {
-            F::template compute<NT>(w, c, tot);
-        } else {
-            f32x16 part[NT];
-#pragma unroll
-            for (int n = 0; n < NT; n++) part[n] = (f32x16){};
-            F::template compute<NT>(w, c, part);
-#pragma unroll
-            for (int n = 0; n < NT; n++) {
-                float S[16], cs[16];
-                col_terms<NT>(c, n, S, cs);
-#pragma unroll
-                for (int i = 0; i < 16; i++) tot[n][i] = fmaf(cs[i], part[n][i], tot[n][i]);
-            }
-        }
+        fold(w, c);
+    }
     }
 #undef JH_LOAD_X
 #undef JH_LOAD_W
