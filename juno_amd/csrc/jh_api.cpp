@@ -188,9 +188,10 @@ int gemv_path();
 std::mutex g_ws_mu;
 std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> g_ws;
 
-// Split-K tile counters of the batched MFMA path, one 4 KB block per
-// (device, stream), zeroed when allocated (so the first use must be eager,
-// like the workspace's); every launch leaves them zero again.
+// Arrival counters of the MFMA split-K hand-off, one block of
+// kCounterSlots 128-byte-spaced counters per (device, stream), zeroed when
+// allocated (so the first use must be eager, like the workspace's); every
+// launch leaves them zero again.
 std::map<std::pair<int, hipStream_t>, int *> g_counters;
 
 int stream_counters(int device, hipStream_t s, int **out) {
@@ -198,9 +199,10 @@ int stream_counters(int device, hipStream_t s, int **out) {
     int *&c = g_counters[{device, s}];
     if (!c) {
         void *p = nullptr;
-        int rc = device_alloc(&p, 4096);
+        const size_t bytes = sizeof(int) * (size_t)jh::kCounterSlots * jh::kCounterStride;
+        int rc = device_alloc(&p, bytes);
         if (rc) return rc;
-        hipError_t e = hipMemset(p, 0, 4096);
+        hipError_t e = hipMemset(p, 0, bytes);
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) {
             (void)hipFree(p);

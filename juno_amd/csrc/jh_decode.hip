@@ -12,6 +12,7 @@
 // captured HIP graph of a whole step can be replayed step after step with the
 // position advanced on the device (pos_increment).
 #include <math.h>
+#include <stdlib.h>
 
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
@@ -425,6 +426,181 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
     }
 }
 
+// One chunk of tc positions for all R query heads of a KV group, with K and V
+// each read once per workgroup and every load issued before the first wait:
+//  * K goes through LDS (as attn_chunk_hd: swizzled float4 rows, lane = row
+//    for q . k); V stays in registers, thread (d4, ph) holding dims 4 d4 .. +4
+//    of rows ph, ph + PH, ...;
+//  * q . k and the softmax weights run one head per wave (waves loop over
+//    the group's heads), the weights of all heads meeting in LDS;
+//  * p . V: each thread folds its V rows into R float4 accumulators (one per
+//    head), the PH row phases are summed through LDS (the K buffer, free by
+//    then) in phase order.
+// The new position's K (roped) and V replace the cache rows in LDS and in the
+// registers and are written to the cache.  Results match attn_chunk_k up to
+// the summation order of p . V.
+template <bool FUSED, int HD, int R>
+__global__ __launch_bounds__(256) void attn_chunk_rv(
+    const float *__restrict__ q, const float *__restrict__ k_new, const float *__restrict__ v_new,
+    float *__restrict__ k_cache, float *__restrict__ v_cache, int n_heads, int n_kv_heads, const int *__restrict__ d_pos,
+    int max_seq, float theta, float scale, float *__restrict__ part, const int *__restrict__ d_slot, int n_slots) {
+    constexpr int tc = 64, Q4 = HD / 4, M = Q4 - 1;
+    constexpr int PH = 256 / Q4;         // row phases of p . V
+    constexpr int VJ = tc / PH;          // V rows per thread
+    constexpr int KJ = tc * Q4 / 256;    // K float4 per thread
+    constexpr int KR = tc * HD > PH * R * HD ? tc * HD : PH * R * HD;  // floats: K rows, later the phase sums
+    extern __shared__ float lds[];
+    float4 *sk4 = reinterpret_cast<float4 *>(lds);  // [tc][Q4] swizzled
+    float *red = lds;                               // [PH][R][HD] after q . k
+    float *srope = lds + KR;                        // [HD / 2] (cos, sin)
+    float *sq = srope + HD;                         // [R][HD]
+    float *sp = sq + R * HD;                        // [R][tc]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int z = blockIdx.z, kv_dim = n_kv_heads * HD;
+    q += (size_t)z * n_heads * HD;
+    if (FUSED) {
+        k_new += (size_t)z * kv_dim;
+        v_new += (size_t)z * kv_dim;
+    }
+    {
+        const size_t cb = d_slot ? (size_t)min(max(d_slot[z], 0), n_slots - 1) * max_seq * kv_dim : 0;
+        k_cache += cb;
+        v_cache += cb;
+    }
+    part += (size_t)z * n_heads * gridDim.y * (HD + 2);
+    const int pos = min(d_pos[z], max_seq - 1), T = pos + 1;
+    const int g = blockIdx.x, c = blockIdx.y, t0 = c * tc;
+    if (t0 >= T) return;  // uniform across the workgroup
+    const int nt = min(tc, T - t0);
+    const bool has_pos = FUSED && pos < t0 + tc;
+    // every K and V load of the chunk in flight at once (rows past the end clamped)
+    float4 kk[KJ], vv[VJ];
+#pragma unroll
+    for (int u = 0; u < KJ; u++) {
+        const int i = u * 256 + tid, t = i / Q4, j = i % Q4;
+        kk[u] = *reinterpret_cast<const float4 *>(k_cache + (size_t)min(t0 + t, T - 1) * kv_dim + g * HD + 4 * j);
+    }
+    const int d4 = tid % Q4, ph = tid / Q4;
+#pragma unroll
+    for (int u = 0; u < VJ; u++) {
+        const int t = ph + PH * u;
+        vv[u] = *reinterpret_cast<const float4 *>(v_cache + (size_t)min(t0 + t, T - 1) * kv_dim + g * HD + 4 * d4);
+    }
+    if (FUSED) {  // rope's (cos, sin) for this position (rope_pair's arithmetic), while the loads fly
+        // every thread computes (no branch for the loads above to sink into); the first HD / 2 store
+        const int pp = tid & (HD / 2 - 1);
+        const double freq = 1.0 / pow((double)theta, (2.0 * pp) / HD);
+        const double angle = pos * freq;
+        const float cs = (float)cos(angle), sn = (float)sin(angle);
+        if (tid < HD / 2) {
+            srope[2 * pp] = cs;
+            srope[2 * pp + 1] = sn;
+        }
+    }
+    // every thread stores every row it loaded (rows past the chunk's end and the
+    // new position's row go to a dummy slot): a conditional store would let the
+    // compiler sink each load into its branch and wait for them one by one
+    float4 *sdummy = reinterpret_cast<float4 *>(sp + R * tc);
+#pragma unroll
+    for (int u = 0; u < KJ; u++) {
+        const int i = u * 256 + tid, t = i / Q4, j = i % Q4;
+        const bool keep = t < nt && !(has_pos && t0 + t == pos);
+        *(keep ? sk4 + t * Q4 + (j ^ (t & M)) : sdummy) = kk[u];
+    }
+    if (has_pos) {
+        const int tp = pos - t0;
+        float *skf = reinterpret_cast<float *>(sk4);
+        if (tid < HD / 2) {  // thread tid wrote pair tid of the table
+            const int p = tid;
+            float ka = k_new[g * HD + 2 * p], kb = k_new[g * HD + 2 * p + 1];
+            rope_rot(ka, kb, srope[2 * p], srope[2 * p + 1]);
+            const int d = 2 * p, slot = tp * Q4 + ((d >> 2) ^ (tp & M));
+            skf[4 * slot + (d & 3)] = ka;
+            skf[4 * slot + (d & 3) + 1] = kb;
+            const size_t o = (size_t)pos * kv_dim + g * HD + 2 * p;
+            k_cache[o] = ka;
+            k_cache[o + 1] = kb;
+        }
+        if (tid < Q4)
+            *reinterpret_cast<float4 *>(v_cache + (size_t)pos * kv_dim + g * HD + 4 * tid) =
+                *reinterpret_cast<const float4 *>(v_new + g * HD + 4 * tid);
+#pragma unroll
+        for (int u = 0; u < VJ; u++)
+            if (ph + PH * u == tp) vv[u] = *reinterpret_cast<const float4 *>(v_new + g * HD + 4 * d4);
+    }
+    __syncthreads();
+    for (int r = wave; r < R; r += 4) {  // wave-uniform
+        const int h = g * R + r;
+        float *sqr = sq + r * HD;
+        for (int p = lane; p < HD / 2; p += 64) {
+            float a = q[h * HD + 2 * p], b = q[h * HD + 2 * p + 1];
+            if (FUSED) rope_rot(a, b, srope[2 * p], srope[2 * p + 1]);
+            sqr[2 * p] = a;
+            sqr[2 * p + 1] = b;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // lanes past the chunk's end compute on whatever row they hold and are masked
+        const float4 *q4 = reinterpret_cast<const float4 *>(sqr);
+        const float4 *k4 = sk4 + lane * Q4;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+        for (int j = 0; j < Q4; j++) {
+            const float4 qq = q4[j], kq = k4[j ^ (lane & M)];
+            a0 = fmaf(qq.x, kq.x, a0);
+            a1 = fmaf(qq.y, kq.y, a1);
+            a2 = fmaf(qq.z, kq.z, a2);
+            a3 = fmaf(qq.w, kq.w, a3);
+        }
+        const float sc = lane < nt ? ((a0 + a1) + (a2 + a3)) * scale : -INFINITY;
+        float m = sc;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float e = lane < nt ? (float)exp((double)(sc - m)) : 0.f;
+        const float l = wave_sum(e);
+        sp[r * tc + lane] = e;  // one weight per position (0 past the chunk's end)
+        if (lane == 0) {
+            float *hp = part + ((size_t)h * gridDim.y + c) * (HD + 2);
+            hp[0] = m;
+            hp[1] = l;
+        }
+    }
+    __syncthreads();  // every head's weights are in LDS; K is no longer read
+    float4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < VJ; u++) {
+        const int t = ph + PH * u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float pw = sp[r * tc + t];
+            acc[r].x = fmaf(pw, vv[u].x, acc[r].x);
+            acc[r].y = fmaf(pw, vv[u].y, acc[r].y);
+            acc[r].z = fmaf(pw, vv[u].z, acc[r].z);
+            acc[r].w = fmaf(pw, vv[u].w, acc[r].w);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) *reinterpret_cast<float4 *>(red + (ph * R + r) * HD + 4 * d4) = acc[r];
+    __syncthreads();
+    for (int i = tid; i < R * HD; i += 256) {
+        const int r = i / HD, d = i % HD;
+        float o = 0.f;
+#pragma unroll
+        for (int k = 0; k < PH; k++) o += red[(k * R + r) * HD + d];
+        part[((size_t)(g * R + r) * gridDim.y + c) * (HD + 2) + 2 + d] = o;
+    }
+}
+
+template <int HD, int R>
+constexpr size_t attn_rv_lds() {
+    constexpr int tc = 64, PH = 256 / (HD / 4);
+    constexpr int KR = tc * HD > PH * R * HD ? tc * HD : PH * R * HD;
+    return sizeof(float) * (KR + HD + R * HD + R * tc + 4);
+}
+
 __global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ part, int head_dim,
                                                       const int *__restrict__ d_pos, int max_seq, int nchmax,
                                                       float *__restrict__ out) {
@@ -527,6 +703,14 @@ hipError_t launch_rope_kv(float *q, const float *k, const float *v, int n_heads,
 
 // V read from the cache instead of LDS: measured at position 511, head_dim 128
 // B = 32 48.2 -> 45.3 us; slower for head_dim 64 (20.6 -> 29.5 us) and at B = 1
+// JUNO_ATTN_RV=0 selects the per-wave kernels (tuning runs)
+static bool attn_rv_wanted() {
+    static const bool on = [] {
+        const char *v = getenv("JUNO_ATTN_RV");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
 static bool attn_v_global(int head_dim, int batch) { return head_dim == 128 && batch >= 8; }
 
 size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq, int batch) {
@@ -563,7 +747,28 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
         return ok;
     }();
     (void)attr;
-    if (head_dim == 64 || head_dim == 128) {
+    const int R = n_heads / n_kv_heads;
+    if ((head_dim == 64 || head_dim == 128) && (R == 1 || R == 2 || R == 4 || R == 8) && attn_rv_wanted()) {
+        // (at most ~40 KB of LDS: within the default dynamic limit)
+#define JH_RV(FU, HD, RR)                                                                                          \
+    attn_chunk_rv<FU, HD, RR><<<grid, 256, attn_rv_lds<HD, RR>(), s>>>(                                             \
+        q, FU ? k_new : nullptr, FU ? v_new : nullptr, k_cache, v_cache, n_heads, n_kv_heads, d_pos, max_seq, theta, \
+        scale, part, d_slot, n_slots)
+#define JH_RV_R(FU, HD)                                                                                            \
+    switch (R) {                                                                                                   \
+    case 1: JH_RV(FU, HD, 1); break;                                                                               \
+    case 2: JH_RV(FU, HD, 2); break;                                                                               \
+    case 4: JH_RV(FU, HD, 4); break;                                                                               \
+    default: JH_RV(FU, HD, 8); break;                                                                              \
+    }
+        if (head_dim == 64) {
+            if (fused) { JH_RV_R(true, 64) } else { JH_RV_R(false, 64) }
+        } else {
+            if (fused) { JH_RV_R(true, 128) } else { JH_RV_R(false, 128) }
+        }
+#undef JH_RV_R
+#undef JH_RV
+    } else if (head_dim == 64 || head_dim == 128) {
         // many workgroups (a batch): V is read from the cache, so that a workgroup's LDS holds only K and more of
         // them fit per CU
         const bool vg = attn_v_global(head_dim, batch);

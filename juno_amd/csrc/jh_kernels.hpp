@@ -103,6 +103,11 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
                             int n_heads, int n_kv_heads, int head_dim, const int *d_pos, int max_seq, float theta,
                             bool fused, float *out, void *workspace, hipStream_t s, int batch = 1,
                             const int *d_slot = nullptr, int n_slots = 1);
+// Arrival counters of the MFMA split-K hand-off: kCounterSlots per stream, one
+// 128-byte line each, so that workgroups arriving at different counters never
+// queue on one line's atomics.  Every launch leaves the counters it used at zero.
+constexpr int kCounterSlots = 1024;
+constexpr int kCounterStride = 32;  // ints
 hipError_t launch_silu_mul(const float *gate, const float *up, int n, float *out, hipStream_t s);
 // y[b] += scale * B (A x[b]) for b < batch; h_ws holds batch * rank floats.
 hipError_t launch_lora(const float *a, const float *b, int rank, int in_dim, int out_dim, float scale, const float *x,

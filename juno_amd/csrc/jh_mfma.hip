@@ -611,7 +611,7 @@ struct FmtQ3K {
 // increment avoid a device-scope release, which on a multi-XCD part writes
 // back the whole L2 (~100 us per workgroup measured); a separate reduction
 // launch costs ~5 us.
-constexpr int kMaxTileCounters = 1024;
+constexpr int kMaxTileCounters = kCounterSlots;
 
 template <int NT>
 __device__ __forceinline__ void store_tile(const f32x16 (&tot)[NT], int r, int nrows, int kh, int B, float *__restrict__ Y,
@@ -643,9 +643,9 @@ __device__ __forceinline__ void store_tile(const f32x16 (&tot)[NT], int r, int n
     __shared__ int s_last;
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int old = __hip_atomic_fetch_add(counters + tile * kCounterStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int last = old == ksplit - 1;
-        if (last) __hip_atomic_store(counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (last) __hip_atomic_store(counters + tile * kCounterStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = last;
     }
     __syncthreads();
@@ -882,7 +882,7 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
 #undef JH_LOAD_X
 #undef JH_LOAD_W
 
-    store_tile<NT>(tot, rbase + c.lr, nrows, c.kh, B, P.y, g.part + P.part0, g.counters + P.cnt0, tile, split,
+    store_tile<NT>(tot, rbase + c.lr, nrows, c.kh, B, P.y, g.part + P.part0, g.counters + (size_t)P.cnt0 * kCounterStride, tile, split,
                    g.ksplit);
 }
 
