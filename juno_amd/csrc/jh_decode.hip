@@ -701,8 +701,6 @@ hipError_t launch_rope_kv(float *q, const float *k, const float *v, int n_heads,
     return hipGetLastError();
 }
 
-// V read from the cache instead of LDS: measured at position 511, head_dim 128
-// B = 32 48.2 -> 45.3 us; slower for head_dim 64 (20.6 -> 29.5 us) and at B = 1
 // JUNO_ATTN_RV=0 selects the per-wave kernels (tuning runs)
 static bool attn_rv_wanted() {
     static const bool on = [] {
@@ -711,6 +709,9 @@ static bool attn_rv_wanted() {
     }();
     return on;
 }
+// per-wave kernels: V read from the cache instead of LDS (measured at position
+// 511, head_dim 128, B = 32: 48.2 -> 45.3 us; slower for head_dim 64, 20.6 ->
+// 29.5 us, and at B = 1)
 static bool attn_v_global(int head_dim, int batch) { return head_dim == 128 && batch >= 8; }
 
 size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq, int batch) {
