@@ -550,7 +550,7 @@ def main():
     log(f"B=1 step: {ms:.4f} ms (wall {wall_ms:.4f} ms, {nlaunch} grouped launches)  {gbs:.1f} GB/s  "
         f"{1e3 / ms:.1f} tok/s")
 
-    avg_ms, per_launch, _ = dominant_kernel(torch, L, mats, stream, reps=max(args.steps // 5, 4))
+    avg_ms, per_launch, _ = dominant_kernel(torch, L, mats, stream, reps=max(args.steps, 20))
     ach = per_launch / (avg_ms * 1e-3) / 1e9
     log(f"gate+up Q4_K grouped GEMV: {avg_ms * 1e3:.2f} us/launch  {ach:.1f} GB/s")
 
