@@ -148,6 +148,16 @@ int jh_qmat_dequant_dev(const jh_qmat *m, float *d_out, void *stream);
 int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *d_x, float *const *d_y,
                          void *stream);
 
+/* out[r] = silu(gate_r . x) * (up_r . x) at B = 1 for every row r of the two
+ * matrices (same shape and format): the FFN's gate / up projections and the
+ * SwiGLU product of LlamaTransformerHandler.java:796-797 (silu: :1733-1735),
+ * which the reference runs as two matVecs and a host loop.  Large matrices
+ * take one staged launch that pairs row r of gate with row r of up, so the
+ * product is formed where both dot products end and neither projection is
+ * written out; otherwise a grouped GEMV into the stream's workspace and
+ * jh_silu_mul_dev's kernel.  Equal to that pair of calls. */
+int jh_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_x, float *d_out, void *stream);
+
 /* Batched form of jh_qmatvec_group_dev: Y_i[B][rows_i] = X_i[B][cols] W_i^T
  * for n <= 4 matrices, full row ranges, one launch when B >= 3 and the
  * matrices share cols (the MFMA path; formats may differ, e.g. the Q4_K q / k

@@ -601,6 +601,35 @@ int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *
     return ok();
 }
 
+int jh_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_x, float *d_out, void *stream) {
+    int rc;
+    if ((rc = check_qmat(gate)) || (rc = check_qmat(up))) return rc;
+    if (!d_x || !d_out) return fail(JH_EINVAL, "x and out must not be null");
+    if (gate->rows != up->rows || gate->cols != up->cols)
+        return fail(JH_EINVAL, "gate [%d x %d] and up [%d x %d] differ in shape", gate->rows, gate->cols, up->rows,
+                    up->cols);
+    if (gate->ctx->device != up->ctx->device) return fail(JH_EINVAL, "matrices on different devices");
+    hipStream_t s = (hipStream_t)stream;
+    const jh::GroupProblem g{gate->type, gate->d_raw, gate->pitch, gate->cols, gate->rows, d_x, nullptr, 0, 0};
+    const jh::GroupProblem u{up->type, up->d_raw, up->pitch, up->cols, up->rows, d_x, nullptr, 0, 0};
+    if (gate->type != JH_TYPE_F32 && gemv_path() != 1) {
+        hipError_t e = jh::launch_gemv_swiglu(g, u, d_out, s);
+        if (e == hipSuccess) return ok();
+        if (e != hipErrorNotSupported) return hip_fail("gemv_swiglu launch", e);
+    }
+    // the two projections into the stream's workspace, then the product
+    void *ws = nullptr;
+    if ((rc = stream_workspace(gate->ctx->device, s, 2 * sizeof(float) * (size_t)gate->rows, &ws))) return rc;
+    float *yg = static_cast<float *>(ws), *yu = yg + gate->rows;
+    const jh_qmat *mats[2] = {gate, up};
+    const float *xs[2] = {d_x, d_x};
+    float *ys[2] = {yg, yu};
+    if ((rc = jh_qmatvec_group_dev(2, mats, xs, ys, stream))) return rc;
+    hipError_t e = jh::launch_silu_mul(yg, yu, gate->rows, d_out, s);
+    if (e != hipSuccess) return hip_fail("silu_mul launch", e);
+    return ok();
+}
+
 int jh_qmatvec_batched_group_dev(int n, const jh_qmat *const *mats, const float *const *d_X, int B,
                                  float *const *d_Y, void *stream) {
     if (n < 0 || n > jh::kMaxMfmaGroup) return fail(JH_EINVAL, "n=%d outside [0, %d]", n, jh::kMaxMfmaGroup);

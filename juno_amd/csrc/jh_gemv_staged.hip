@@ -469,7 +469,14 @@ struct StagedArgs {
     int gw;   // waves per row group (column tiles): 1, 2 or 4
     int tb;   // blocks per tile
     const float *x;
+    float *swiglu;  // not null: w = {gate, up} interleaved row by row, out = silu(gate . x) * (up . x)
 };
+
+// SwiGLU pairing: virtual row v is row v / 2 of gate (v even) or up (v odd),
+// so that a row group (R even) holds both halves of its outputs.
+__device__ __forceinline__ float silu_times(float g, float u) {
+    return g / (1.f + (float)exp(-(double)g)) * u;  // silu_mul_k's arithmetic
+}
 
 __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
     int p = 0;
@@ -538,8 +545,9 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
 #pragma unroll
         for (int i = 0; i < R; i++) {
             const int vr = min(r0 + i, nrows - 1);
-            const int p = staged_problem(args, vr);
-            const size_t off = (size_t)(args.row0[p] + vr - args.cum[p]) * pitch + tile_off;
+            const int p = args.swiglu ? (vr & 1) : staged_problem(args, vr);
+            const int rr = args.swiglu ? (vr >> 1) : vr - args.cum[p];
+            const size_t off = (size_t)(args.row0[p] + rr) * pitch + tile_off;
             start[i] = (int)(off & 15);
             const uint8_t *base = args.w[p] + (off & ~size_t(15));
 #pragma unroll
@@ -596,10 +604,17 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
             args.y[p][vr - args.cum[p]] = val;
         };
         if (gw == 1) {
-            if (lane == 63)
+            if (lane == 63) {
+                if (args.swiglu) {
 #pragma unroll
-                for (int i = 0; i < R; i++)
-                    if (r0 + i < nrows) store(r0 + i, s[i]);
+                    for (int i = 0; i + 1 < R; i += 2)
+                        if (r0 + i < nrows) args.swiglu[(r0 + i) >> 1] = silu_times(s[i], s[i + 1]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < R; i++)
+                        if (r0 + i < nrows) store(r0 + i, s[i]);
+                }
+            }
             if (next >= ngroups) break;
         } else {
             float *pp = part + (it & 1) * 4 * R;
@@ -607,13 +622,23 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
 #pragma unroll
                 for (int i = 0; i < R; i++) pp[wave * R + i] = s[i];
             __syncthreads();
-            if (tile == 0 && lane == 63 && grp < ngroups)
+            if (tile == 0 && lane == 63 && grp < ngroups) {
+                float t[R];
 #pragma unroll
                 for (int i = 0; i < R; i++) {
-                    float t = 0.f;
-                    for (int q = 0; q < gw; q++) t += pp[(slot * gw + q) * R + i];
-                    if (r0 + i < nrows) store(r0 + i, t);
+                    t[i] = 0.f;
+                    for (int q = 0; q < gw; q++) t[i] += pp[(slot * gw + q) * R + i];
                 }
+                if (args.swiglu) {
+#pragma unroll
+                    for (int i = 0; i + 1 < R; i += 2)
+                        if (r0 + i < nrows) args.swiglu[(r0 + i) >> 1] = silu_times(t[i], t[i + 1]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < R; i++)
+                        if (r0 + i < nrows) store(r0 + i, t[i]);
+                }
+            }
             // every wave of the workgroup iterates while slot 0 has work
             if (next - slot >= ngroups) break;
         }
@@ -725,6 +750,27 @@ hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s) {
     sa.cols = a.cols;
     sa.x = a.x;
     return launch_staged_any(sa, a.type, s);
+}
+
+hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, float *out, hipStream_t s) {
+    const int R = staged_rows(2);
+    if (R % 2 || gate.type != up.type || gate.cols != up.cols || gate.pitch != up.pitch || gate.x != up.x ||
+        gate.nrows != up.nrows || gate.nrows < 1 || !staged_supported(gate.type, gate.cols))
+        return hipErrorNotSupported;
+    if (!staged_wanted(2 * (size_t)gate.nrows * gate.pitch)) return hipErrorNotSupported;
+    StagedArgs sa = {};
+    sa.np = 2;
+    sa.w[0] = gate.w;
+    sa.w[1] = up.w;
+    sa.cum[1] = gate.nrows;
+    sa.cum[2] = 2 * gate.nrows;
+    sa.pitch = gate.pitch;
+    sa.nb = gate.type == 8 ? gate.cols / 32 : gate.cols / 256;
+    sa.nrows = 2 * gate.nrows;
+    sa.cols = gate.cols;
+    sa.x = gate.x;
+    sa.swiglu = out;
+    return launch_staged_any(sa, gate.type, s);
 }
 
 hipError_t launch_gemv_staged_group(int n, const GroupProblem *p, hipStream_t s) {

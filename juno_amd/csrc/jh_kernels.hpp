@@ -49,6 +49,10 @@ hipError_t launch_gemv_group(GroupArgs g, hipStream_t s);
 // hipErrorNotSupported when the problems do not qualify.
 constexpr int kMaxStagedGroup = 4;
 hipError_t launch_gemv_staged_group(int n, const GroupProblem *p, hipStream_t s);
+// out[r] = silu(gate_r . x) * (up_r . x) for every row r, B = 1, one staged
+// launch that takes a row of gate and the same row of up into one row group
+// (hipErrorNotSupported where the staged kernel does not apply)
+hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, float *out, hipStream_t s);
 
 // B = 1 coalesced, pipelined, int8-x kernel (jh_gemv_staged.hip); returns
 // hipErrorNotSupported for shapes it does not cover.

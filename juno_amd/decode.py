@@ -263,8 +263,6 @@ class LlamaDecoder:
         self.v = torch.zeros(c.kv_dim, **f32)
         self.att = torch.zeros(c.hidden_dim, **f32)
         self.proj = torch.zeros(c.hidden_dim, **f32)
-        self.gate = torch.zeros(c.intermediate_size, **f32)
-        self.up = torch.zeros(c.intermediate_size, **f32)
         self.hid = torch.zeros(c.intermediate_size, **f32)
         self.logits = torch.zeros(c.vocab_size, **f32)
         self.pos = torch.zeros(1, device=dev, dtype=torch.int32)
@@ -313,8 +311,8 @@ class LlamaDecoder:
             self._group([m["o"]], [self.att], [self.proj], s)
             # x2 = x + attnProj (:778); rmsNorm(x2) (:781)
             _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(lw.ffn_norm), H, eps, P(self.x), P(self.xn), s))
-            self._group([m["gate"], m["up"]], [self.xn] * 2, [self.gate, self.up], s)
-            _check(L.jh_silu_mul_dev(P(self.gate), P(self.up), c.intermediate_size, P(self.hid), s))
+            # silu(gate . x2n) * (up . x2n) (:796-797): one launch pairs each gate row with its up row
+            _check(L.jh_qmatvec_swiglu_dev(m["gate"].handle, m["up"].handle, P(self.xn), P(self.hid), s))
             self._group([m["down"]], [self.hid], [self.proj], s)
         # final residual, rmsNorm(x, outputNorm) and the output projection (:803-810)
         _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(self.w.output_norm), H, eps, P(self.x), P(self.xn), s))

@@ -565,3 +565,40 @@ def test_group_dev_arguments(be):
     assert "n=9" in _lib.last_error()
     assert L.jh_qmatvec_group_dev(1, None, None, None, None) == _lib.JH_EINVAL
     be.sgemv_group_dev([], [], [])  # n = 0 is a no-op
+
+
+@pytest.mark.parametrize("qt,rows,cols", [(O.Q4_K, 8192, 4096), (O.Q6_K, 1536, 14336), (O.Q4_K, 256, 1024),
+                                          (O.Q8_0, 300, 2048)],
+                         ids=["q4k staged", "q6k staged 4 tiles", "q4k small", "q8_0 small"])
+def test_swiglu_dev(be, qt, rows, cols):
+    """jh_qmatvec_swiglu_dev equals jh_qmatvec_group_dev on [gate, up] followed by
+    jh_silu_mul_dev, bit for bit (the paired staged launch forms each row's
+    two dot products exactly as the grouped launch does); the projections
+    themselves are pinned against the oracle by the group tests."""
+    import ctypes
+    import torch
+    from juno_amd import _lib
+    L = _lib.load()
+    say("swiglu", qt, rows, cols)
+    raw_g = O.quantize(qt, weights(rows * cols, 400 + qt))
+    raw_u = O.quantize(qt, weights(rows * cols, 401 + qt))
+    g, u = upload(be, qt, raw_g, rows, cols), upload(be, qt, raw_u, rows, cols)
+    try:
+        x = torch.from_numpy(vec(cols, 402) * 3).cuda()
+        yg = torch.full((rows,), float("nan"), device="cuda")
+        yu = torch.full((rows,), float("nan"), device="cuda")
+        ref = torch.full((rows,), float("nan"), device="cuda")
+        out = torch.full((rows,), float("nan"), device="cuda")
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        be.sgemv_group_dev([g, u], [x.data_ptr()] * 2, [yg.data_ptr(), yu.data_ptr()])
+        assert L.jh_silu_mul_dev(P(yg), P(yu), rows, P(ref), None) == 0
+        assert L.jh_qmatvec_swiglu_dev(g.handle, u.handle, P(x), P(out), None) == 0, L.jh_last_error()
+        torch.cuda.synchronize()
+        assert torch.isfinite(ref).all()
+        assert torch.equal(out, ref)
+        # mismatched shapes are refused
+        with upload(be, qt, raw_g[: len(raw_g) // 2], rows // 2, cols) as half:
+            assert L.jh_qmatvec_swiglu_dev(g.handle, half.handle, P(x), P(out), None) == 1
+    finally:
+        g.close()
+        u.close()
