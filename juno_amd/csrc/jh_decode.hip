@@ -41,12 +41,21 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_k(const float *x, const 
     constexpr int kKeep = 8;
     float keep[kKeep];
     float ss = 0.f;
+    // every load of the thread's values first (addresses clamped in range), so
+    // that they are in flight together rather than one per branch
+    float xr[kKeep], rr[kKeep];
+#pragma unroll
+    for (int k = 0; k < kKeep; k++) {
+        const int i = min(threadIdx.x + k * kNormThreads, n - 1);
+        xr[k] = x[i];
+        rr[k] = res ? res[i] : 0.f;
+    }
 #pragma unroll
     for (int k = 0; k < kKeep; k++) {
         const int i = threadIdx.x + k * kNormThreads;
         float v = 0.f;
         if (i < n) {
-            v = res ? x[i] + res[i] : x[i];
+            v = res ? xr[k] + rr[k] : xr[k];
             if (x_out) x_out[i] = v;
         }
         keep[k] = v;
@@ -604,28 +613,52 @@ constexpr size_t attn_rv_lds() {
 __global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ part, int head_dim,
                                                       const int *__restrict__ d_pos, int max_seq, int nchmax,
                                                       float *__restrict__ out) {
-    __shared__ float wc[1024];
+    // The chunk maxima and normalisers are loaded by one thread per chunk, all at
+    // once; the sums over chunks then run in chunk order from LDS (L) or with
+    // eight chunks' loads in flight (o), so that the arithmetic is the plain
+    // sequential one without a memory round trip per chunk.
+    __shared__ float wc[1024], wl[1024], wmax[4];
     __shared__ float sL;
     const int h = blockIdx.x, tc = attn_tc(head_dim), z = blockIdx.y;  // head, request
+    const int tid = threadIdx.x;
     d_pos += z;
     part += (size_t)z * gridDim.x * nchmax * (head_dim + 2);
     out += (size_t)z * gridDim.x * head_dim;
     const int T = min(*d_pos, max_seq - 1) + 1, nch = min((T + tc - 1) / tc, 1024);
     const float *ph = part + (size_t)h * nchmax * (head_dim + 2);
     float M = -INFINITY;
-    for (int c = 0; c < nch; c++) M = fmaxf(M, ph[c * (head_dim + 2)]);
-    for (int c = threadIdx.x; c < nch; c += 256) wc[c] = (float)exp((double)(ph[c * (head_dim + 2)] - M));
+    for (int c = tid; c < nch; c += 256) {
+        const float m = ph[c * (head_dim + 2)];
+        wc[c] = m;
+        wl[c] = ph[c * (head_dim + 2) + 1];
+        M = fmaxf(M, m);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    if ((tid & 63) == 0) wmax[tid >> 6] = M;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));  // max: any order gives the same value
+    for (int c = tid; c < nch; c += 256) wc[c] = (float)exp((double)(wc[c] - M));
+    __syncthreads();
+    if (tid == 0) {
         float L = 0.f;
-        for (int c = 0; c < nch; c++) L += ph[c * (head_dim + 2) + 1] * wc[c];
+        for (int c = 0; c < nch; c++) L += wl[c] * wc[c];
         sL = L;
     }
     __syncthreads();
     const float L = sL;
-    for (int d = threadIdx.x; d < head_dim; d += 256) {
+    for (int d = tid; d < head_dim; d += 256) {
+        const float *op = ph + 2 + d;
         float o = 0.f;
-        for (int c = 0; c < nch; c++) o += ph[c * (head_dim + 2) + 2 + d] * wc[c];
+        int c = 0;
+        for (; c + 8 <= nch; c += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = op[(c + u) * (head_dim + 2)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) o += v[u] * wc[c + u];
+        }
+        for (; c < nch; c++) o += op[c * (head_dim + 2)] * wc[c];
         out[(size_t)h * head_dim + d] = o / L;
     }
 }
