@@ -158,6 +158,15 @@ int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *
  * jh_silu_mul_dev's kernel.  Equal to that pair of calls. */
 int jh_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_x, float *d_out, void *stream);
 
+/* Batched form: out[b][r] = silu(gate_r . X_b) * (up_r . X_b) for B rows of X.
+ * For 3 <= B <= 32 (Q4_K, Q5_K, Q6_K, Q8_0) one MFMA launch whose workgroups
+ * take 128 rows of gate and the same rows of up and store the product; B = 1
+ * is jh_qmatvec_swiglu_dev; otherwise jh_qmatvec_batched_group_dev into the
+ * caller's d_gate / d_up scratch ([B][rows] each, used only on that path) and
+ * jh_silu_mul_dev.  Equal to that pair of calls, bit for bit. */
+int jh_qmatvec_batched_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_X, int B, float *d_out,
+                                  float *d_gate, float *d_up, void *stream);
+
 /* Batched form of jh_qmatvec_group_dev: Y_i[B][rows_i] = X_i[B][cols] W_i^T
  * for n <= 4 matrices, full row ranges, one launch when B >= 3 and the
  * matrices share cols (the MFMA path; formats may differ, e.g. the Q4_K q / k

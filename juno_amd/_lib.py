@@ -40,6 +40,7 @@ SIGNATURES = {
     "jh_qmatvec_group_dev": (_I, [_I, _P, _P, _P, _P]),
     "jh_qmatvec_batched_group_dev": (_I, [_I, _P, _P, _I, _P, _P]),
     "jh_qmatvec_swiglu_dev": (_I, [_P, _P, _P, _P, _P]),
+    "jh_qmatvec_batched_swiglu_dev": (_I, [_P, _P, _P, _I, _P, _P, _P, _P]),
     "jh_quantize_dev": (_I, [_I, _P, ctypes.c_int64, _P, _P]),
     "jh_rmsnorm_dev": (_I, [_P, _P, _P, _I, ctypes.c_float, _P, _P, _P]),
     "jh_rope_kv_dev": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P]),

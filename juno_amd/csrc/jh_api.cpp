@@ -630,6 +630,41 @@ int jh_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d
     return ok();
 }
 
+int jh_qmatvec_batched_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_X, int B, float *d_out,
+                                  float *d_gate, float *d_up, void *stream) {
+    int rc;
+    if ((rc = check_qmat(gate)) || (rc = check_qmat(up))) return rc;
+    if (B < 0) return fail(JH_EINVAL, "B=%d must be >= 0", B);
+    if (B == 0) return ok();
+    if (!d_X || !d_out) return fail(JH_EINVAL, "X and out must not be null");
+    if (gate->rows != up->rows || gate->cols != up->cols)
+        return fail(JH_EINVAL, "gate [%d x %d] and up [%d x %d] differ in shape", gate->rows, gate->cols, up->rows,
+                    up->cols);
+    if (gate->ctx->device != up->ctx->device) return fail(JH_EINVAL, "matrices on different devices");
+    if (B == 1) return jh_qmatvec_swiglu_dev(gate, up, d_X, d_out, stream);
+    hipStream_t s = (hipStream_t)stream;
+    const jh::MfmaDesc dg{gate->type, gate->d_raw, gate->pitch, gate->cols, 0, gate->rows, d_X, nullptr};
+    const jh::MfmaDesc du{up->type, up->d_raw, up->pitch, up->cols, 0, up->rows, d_X, nullptr};
+    if (jh::mfma_swiglu_applies(dg, du, B)) {
+        const int dev = gate->ctx->device;
+        void *ws = nullptr;
+        int *counters = nullptr;
+        if ((rc = stream_workspace(dev, s, jh::mfma_swiglu_workspace_bytes(dg, B), &ws))) return rc;
+        if ((rc = stream_counters(dev, s, &counters))) return rc;
+        hipError_t e = jh::launch_mfma_swiglu(dg, du, B, d_out, ws, counters, s);
+        if (e == hipSuccess) return ok();
+        if (e != hipErrorNotSupported) return hip_fail("mfma swiglu launch", e);
+    }
+    if (!d_gate || !d_up) return fail(JH_EINVAL, "gate and up scratch must not be null on this path (B=%d)", B);
+    const jh_qmat *mats[2] = {gate, up};
+    const float *xs[2] = {d_X, d_X};
+    float *ys[2] = {d_gate, d_up};
+    if ((rc = jh_qmatvec_batched_group_dev(2, mats, xs, B, ys, stream))) return rc;
+    hipError_t e = jh::launch_silu_mul(d_gate, d_up, B * gate->rows, d_out, s);
+    if (e != hipSuccess) return hip_fail("silu_mul launch", e);
+    return ok();
+}
+
 int jh_qmatvec_batched_group_dev(int n, const jh_qmat *const *mats, const float *const *d_X, int B,
                                  float *const *d_Y, void *stream) {
     if (n < 0 || n > jh::kMaxMfmaGroup) return fail(JH_EINVAL, "n=%d outside [0, %d]", n, jh::kMaxMfmaGroup);

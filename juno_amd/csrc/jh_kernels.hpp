@@ -82,6 +82,13 @@ constexpr int kMaxMfmaGroup = 4;
 constexpr int kMfmaMinBatch = 3;
 size_t mfma_group_workspace_bytes(int n, const MfmaDesc *d, int B);
 hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, int *counters, hipStream_t s);
+// out[b][r] = silu(gate_r . x_b) * (up_r . x_b) for 3 <= B <= 32: one MFMA
+// launch whose workgroups take 128 rows of gate and the same 128 rows of up
+// (Q4_K, Q5_K, Q6_K, Q8_0; full row ranges, same shape and x).
+bool mfma_swiglu_applies(const MfmaDesc &gate, const MfmaDesc &up, int B);
+size_t mfma_swiglu_workspace_bytes(const MfmaDesc &gate, int B);
+hipError_t launch_mfma_swiglu(const MfmaDesc &gate, const MfmaDesc &up, int B, float *out, void *workspace,
+                              int *counters, hipStream_t s);
 
 // out[rows][cols] fp32, bit-exact with the reference dequantizers.
 hipError_t launch_dequant(int type, const uint8_t *w, int rows, int cols, float *out, hipStream_t s);

@@ -707,6 +707,11 @@ struct MfmaGroup {
     float *part;
     int *counters;
     int n, nsb, ksb, ksplit, B;
+    // SwiGLU pairs (mfma_group<.., true>): p[0] is gate, w2 the up matrix of the
+    // same shape; a workgroup's waves 0-3 take 128 gate rows and waves 4-7 the
+    // same up rows, and swiglu[b][r] = silu(gate) * up replaces both outputs
+    const uint8_t *w2;
+    float *swiglu;
 };
 
 // format mask bits: Q4_K, Q5_K, Q6_K, Q8_0, Q2_K, Q3_K
@@ -730,9 +735,85 @@ __host__ __device__ constexpr int lds_bytes() {
     return (NT == 1 ? 2 : 1) * lds_w_offset<NT>() + kWaves * kRowsPerWave * max_chunks<MASK>() * 16 + kWinPad;
 }
 
+__device__ __forceinline__ float silu_times(float g, float u) {
+    return g / (1.f + (float)exp(-(double)g)) * u;  // silu_mul_k's arithmetic
+}
+
+// store_tile for a SwiGLU pair workgroup (B <= 32): split partials over virtual
+// rows (gate r, up rows + r) in planes of B x 2 rows, the usual hand-off, then
+// the up waves pass their totals to the gate waves through LDS and those store
+// silu(gate) * up.  r is the lane's row within its matrix, lw its row within
+// the workgroup's 128.
+__device__ __forceinline__ void store_pair(const f32x16 (&tot)[1], int r, int lw, bool up, int nrows, int kh, int B,
+                                           float *__restrict__ out, float *part, int *counters, int tile, int split,
+                                           int ksplit, uint8_t *lds) {
+    const bool live = r < nrows;
+    const int vr = r + (up ? nrows : 0);
+    float fin[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) fin[i] = tot[0][i];
+    if (ksplit > 1) {
+        const size_t plane = (size_t)B * 2 * nrows;
+        if (live) {
+            float *mine = part + split * plane;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int b = batch_of(0, i, kh);
+                if (b < B) __hip_atomic_store(mine + (size_t)b * 2 * nrows + vr, tot[0][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __shared__ int s_last;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int old = __hip_atomic_fetch_add(counters + tile * kCounterStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int last = old == ksplit - 1;
+            if (last) __hip_atomic_store(counters + tile * kCounterStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last;
+        }
+        __syncthreads();
+        if (!s_last) return;  // uniform across the workgroup
+        constexpr int KB = 4;
+        float acc[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[i] = 0.f;
+        const int rr = min(vr, 2 * nrows - 1);
+        for (int k0 = 0; k0 < ksplit; k0 += KB) {
+            float v[KB][16];
+#pragma unroll
+            for (int kk = 0; kk < KB; kk++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int b = min(batch_of(0, i, kh), B - 1);
+                    v[kk][i] = __hip_atomic_load(part + min(k0 + kk, ksplit - 1) * plane + (size_t)b * 2 * nrows + rr,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+            for (int kk = 0; kk < KB; kk++)
+                if (k0 + kk < ksplit)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) acc[i] += v[kk][i];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) fin[i] = acc[i];
+    }
+    float *xl = reinterpret_cast<float *>(lds);  // [128 rows][33]: the up totals
+    __syncthreads();  // every wave is done with the x buffers
+    if (up)
+#pragma unroll
+        for (int i = 0; i < 16; i++) xl[lw * 33 + batch_of(0, i, kh)] = fin[i];
+    __syncthreads();
+    if (!up && live)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int b = batch_of(0, i, kh);
+            if (b < B) out[(size_t)b * nrows + r] = silu_times(fin[i], xl[lw * 33 + b]);
+        }
+}
+
 // One workgroup's tile (32 rows per wave x all batch columns) over the K
 // range of its split, x converted into LDS super-block by super-block.
-template <class F, int NT, int PD>  // NT = padded batch / 32, PD = weight prefetch depth (super-blocks)
+template <class F, int NT, int PD, bool PAIR>  // NT = padded batch / 32, PD = weight prefetch depth (super-blocks)
 __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int split, const MfmaGroup &g, uint8_t *lds) {
     constexpr int BP = 32 * NT;
     constexpr int CPT = BP / 32;  // x columns converted per thread (16 lanes per column and super-block)
@@ -743,7 +824,8 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
     _Float16 *sh_xs = sh_lo + BP * COLH;
     _Float16 *sh_x16 = sh_xs + BP * 16;
     float2 *sh_S = reinterpret_cast<float2 *>(sh_x16 + BP * 32);  // (sum of x, 1 / column scale) per column
-    const uint8_t *__restrict__ W = P.w;
+    const bool up_half = PAIR && (threadIdx.x >> 6) >= kWaves / 2;  // SwiGLU pairs: waves 4-7 take the up rows
+    const uint8_t *__restrict__ W = up_half ? g.w2 : P.w;
     const float *__restrict__ X = P.x;
     const size_t pitch = P.pitch;
     const int nrows = P.rows, row0 = P.row0, B = g.B, cols = 256 * g.nsb;
@@ -751,7 +833,8 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const Ctx c{wave, lane & 31, lane >> 5, sh_hi, sh_lo, sh_xs, sh_x16, sh_S};
-    const int rbase = tile * kRowsPerWG + wave * kRowsPerWave;
+    const int rbase = PAIR ? tile * (kRowsPerWG / 2) + (wave & (kWaves / 2 - 1)) * kRowsPerWave
+                           : tile * kRowsPerWG + wave * kRowsPerWave;
     const int sb0 = split * g.ksb, sb1 = min(g.nsb, sb0 + g.ksb);
     auto row_off = [&](int rho) { return (size_t)(row0 + min(rbase + rho, nrows - 1)) * pitch; };
     // Weight staging: chunk j = lane + 64 k of the wave's 32 x CH chunk grid is
@@ -882,13 +965,18 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
 #undef JH_LOAD_X
 #undef JH_LOAD_W
 
+    if constexpr (PAIR) {
+        store_pair(tot, rbase + c.lr, (wave & (kWaves / 2 - 1)) * kRowsPerWave + c.lr, up_half, nrows, c.kh, B,
+                   g.swiglu, g.part, g.counters, tile, split, g.ksplit, lds);
+        return;
+    }
     store_tile<NT>(tot, rbase + c.lr, nrows, c.kh, B, P.y, g.part + P.part0, g.counters + (size_t)P.cnt0 * kCounterStride, tile, split,
                    g.ksplit);
 }
 
 // A group of matrices with the same K in one launch (1-D grid): each
 // workgroup finds its matrix and runs that matrix's format.
-template <int NT, int MASK>
+template <int NT, int MASK, bool PAIR = false>
 __global__ __launch_bounds__(kThreads) void mfma_group(MfmaGroup g) {
     __shared__ __align__(16) uint8_t lds[lds_bytes<NT, MASK>()];
     const int id = blockIdx.x;
@@ -899,12 +987,12 @@ __global__ __launch_bounds__(kThreads) void mfma_group(MfmaGroup g) {
     const int local = id - P.wg0, tile = local / g.ksplit, split = local - tile * g.ksplit;
     constexpr int PD = NT == 1 ? kPrefetch : 1;
     switch (P.type) {
-        case 12: if constexpr ((MASK & 1) != 0) gemm_body<FmtQ4K, NT, PD>(P, tile, split, g, lds); break;
-        case 13: if constexpr ((MASK & 2) != 0) gemm_body<FmtQ5K, NT, PD>(P, tile, split, g, lds); break;
-        case 14: if constexpr ((MASK & 4) != 0) gemm_body<FmtQ6K, NT, PD>(P, tile, split, g, lds); break;
-        case 10: if constexpr ((MASK & 16) != 0) gemm_body<FmtQ2K, NT, PD>(P, tile, split, g, lds); break;
-        case 11: if constexpr ((MASK & 32) != 0) gemm_body<FmtQ3K, NT, PD>(P, tile, split, g, lds); break;
-        default: if constexpr ((MASK & 8) != 0) gemm_body<FmtQ8_0, NT, PD>(P, tile, split, g, lds); break;
+        case 12: if constexpr ((MASK & 1) != 0) gemm_body<FmtQ4K, NT, PD, PAIR>(P, tile, split, g, lds); break;
+        case 13: if constexpr ((MASK & 2) != 0) gemm_body<FmtQ5K, NT, PD, PAIR>(P, tile, split, g, lds); break;
+        case 14: if constexpr ((MASK & 4) != 0) gemm_body<FmtQ6K, NT, PD, PAIR>(P, tile, split, g, lds); break;
+        case 10: if constexpr ((MASK & 16) != 0) gemm_body<FmtQ2K, NT, PD, PAIR>(P, tile, split, g, lds); break;
+        case 11: if constexpr ((MASK & 32) != 0) gemm_body<FmtQ3K, NT, PD, PAIR>(P, tile, split, g, lds); break;
+        default: if constexpr ((MASK & 8) != 0) gemm_body<FmtQ8_0, NT, PD, PAIR>(P, tile, split, g, lds); break;
     }
 }
 
@@ -1154,6 +1242,65 @@ static void launch_group_nt(const MfmaGroup &g, int mask, int grid, hipStream_t 
         case 32: mfma_group<NT, 32><<<grid, kThreads, 0, s>>>(g); break;
         default: mfma_group<NT, 63><<<grid, kThreads, 0, s>>>(g); break;
     }
+}
+
+bool mfma_swiglu_applies(const MfmaDesc &gate, const MfmaDesc &up, int B) {
+    if (B < kMfmaMinBatch || B > 32 || gate.type != up.type || gate.cols != up.cols || gate.pitch != up.pitch ||
+        gate.x != up.x || gate.row_start != 0 || up.row_start != 0 || gate.row_end != up.row_end)
+        return false;
+    if (gate.type != 12 && gate.type != 13 && gate.type != 14 && gate.type != 8) return false;
+    if (((reinterpret_cast<uintptr_t>(up.w) | up.pitch) & 15) && (up.type == 12 || up.type == 13)) return false;
+    MfmaDesc v = gate;
+    v.row_end = 2 * gate.row_end;  // the pair's virtual rows: same tiles and K split as one matrix of 2 x rows
+    Plan p;
+    return plan_group(1, &v, B, p) && (p.ksplit == 1 || (gate.row_end + kRowsPerWG / 2 - 1) / (kRowsPerWG / 2) <= kMaxTileCounters);
+}
+
+size_t mfma_swiglu_workspace_bytes(const MfmaDesc &gate, int B) {
+    MfmaDesc v = gate;
+    v.row_end = 2 * gate.row_end;
+    Plan p;
+    if (!plan_group(1, &v, B, p)) return 0;
+    return p.ksplit > 1 ? sizeof(float) * (size_t)p.ksplit * B * v.row_end : 16;
+}
+
+hipError_t launch_mfma_swiglu(const MfmaDesc &gate, const MfmaDesc &up, int B, float *out, void *workspace,
+                              int *counters, hipStream_t s) {
+    if (!mfma_swiglu_applies(gate, up, B)) return hipErrorNotSupported;
+    MfmaDesc v = gate;
+    v.row_end = 2 * gate.row_end;
+    Plan p;
+    plan_group(1, &v, B, p);
+    if (p.ksplit > 1 && !counters) return hipErrorNotSupported;
+    MfmaGroup g = {};
+    g.part = reinterpret_cast<float *>(workspace);
+    g.counters = counters;
+    g.n = 1;
+    g.nsb = p.nsb;
+    g.ksb = p.ksb;
+    g.ksplit = p.ksplit;
+    g.B = B;
+    g.w2 = up.w;
+    g.swiglu = out;
+    MfmaProblem &q = g.p[0];
+    q.w = gate.w;
+    q.x = gate.x;
+    q.y = nullptr;
+    q.pitch = gate.pitch;
+    q.type = gate.type;
+    q.row0 = 0;
+    q.rows = gate.row_end;
+    q.tiles = (q.rows + kRowsPerWG / 2 - 1) / (kRowsPerWG / 2);
+    q.wg0 = q.cnt0 = 0;
+    q.part0 = 0;
+    const int grid = q.tiles * p.ksplit;
+    switch (gate.type) {
+        case 12: mfma_group<1, 1, true><<<grid, kThreads, 0, s>>>(g); break;
+        case 13: mfma_group<1, 2, true><<<grid, kThreads, 0, s>>>(g); break;
+        case 14: mfma_group<1, 4, true><<<grid, kThreads, 0, s>>>(g); break;
+        default: mfma_group<1, 8, true><<<grid, kThreads, 0, s>>>(g); break;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, int *counters, hipStream_t s) {

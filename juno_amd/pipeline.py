@@ -10,9 +10,9 @@ Mirrors the reference's pipeline contract (paths under
 * ``forward_batch(request_ids, all_tokens, start_positions)``
   InferencePipeline.forwardBatch (:47-69): the reference's default is a serial
   loop over forward(); here the N requests are stacked and every layer runs
-  once for all of them (batched GEMVs, [q, k, v] and [gate, up] grouped: the
-  B <= 2 GEMV kernels, fp16 MFMA from B = 3, one launch per group; one batched
-  rope + KV-append + attention launch pair)
+  once for all of them (batched GEMVs, [q, k, v] grouped: the B <= 2 GEMV
+  kernels, fp16 MFMA from B = 3, one launch per group; [gate, up] and SwiGLU in
+  one launch; one batched rope + KV-append + attention launch pair)
 * ``vocab_size()``  InferencePipeline.vocabSize (:71-75)
 * ``evict(request_id)``  LlamaTransformerHandler.evict (:496-504)
 * ``lora``  an optional LoraAdapterSet whose "wq" / "wv" adapters are added after
@@ -173,8 +173,9 @@ class LlamaBatchPipeline:
             gemv(m["o"], self.att, self.proj)
             _check(L.jh_rmsnorm_rows_dev(P(self.x), P(self.proj), P(lw.ffn_norm), H, B, eps, P(self.x), P(self.xn),
                                          s))
-            group([m["gate"], m["up"]], self.xn, [self.gate, self.up])
-            _check(L.jh_silu_mul_dev(P(self.gate), P(self.up), B * I, P(self.hid), s))
+            # silu(gate) * up (LlamaTransformerHandler.java:796-797): one launch pairs gate and up rows
+            _check(L.jh_qmatvec_batched_swiglu_dev(m["gate"].handle, m["up"].handle, P(self.xn), B, P(self.hid),
+                                                   P(self.gate), P(self.up), s))
             gemv(m["down"], self.hid, self.proj)
         _check(L.jh_rmsnorm_rows_dev(P(self.x), P(self.proj), P(self.w.output_norm), H, B, eps, P(self.x),
                                      P(self.xn), s))

@@ -602,3 +602,41 @@ def test_swiglu_dev(be, qt, rows, cols):
     finally:
         g.close()
         u.close()
+
+
+@pytest.mark.parametrize("qt,rows,cols", [(O.Q4_K, 1000, 4096), (O.Q6_K, 384, 2048), (O.Q5_K, 256, 1024),
+                                          (O.Q8_0, 300, 3072), (O.Q4_K, 4096, 14336)],
+                         ids=["q4k", "q6k", "q5k", "q8_0", "q4k split K"])
+@pytest.mark.parametrize("B", [1, 2, 3, 17, 32, 40])
+def test_batched_swiglu_dev(be, qt, rows, cols, B):
+    """jh_qmatvec_batched_swiglu_dev equals jh_qmatvec_batched_group_dev on
+    [gate, up] followed by jh_silu_mul_dev, bit for bit, at every batch: the
+    paired MFMA launch (3 <= B <= 32, a row count that is not a multiple of its
+    128-row tiles, split K at 14336 columns), B = 1 and the fallback (B = 2, 40)."""
+    import ctypes
+    import torch
+    from juno_amd import _lib
+    L = _lib.load()
+    say("batched swiglu", qt, rows, cols, B)
+    raw_g = O.quantize(qt, weights(rows * cols, 410 + qt))
+    raw_u = O.quantize(qt, weights(rows * cols, 411 + qt))
+    g, u = upload(be, qt, raw_g, rows, cols), upload(be, qt, raw_u, rows, cols)
+    try:
+        X = torch.from_numpy(vec(cols, 412, batch=B) * 3).cuda()
+        yg = torch.full((B, rows), float("nan"), device="cuda")
+        yu = torch.full((B, rows), float("nan"), device="cuda")
+        ref = torch.full((B, rows), float("nan"), device="cuda")
+        out = torch.full((B, rows), float("nan"), device="cuda")
+        sg = torch.full((B, rows), float("nan"), device="cuda")
+        su = torch.full((B, rows), float("nan"), device="cuda")
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        be.sgemv_batched_group_dev([g, u], [X.data_ptr()] * 2, B, [yg.data_ptr(), yu.data_ptr()])
+        assert L.jh_silu_mul_dev(P(yg), P(yu), B * rows, P(ref), None) == 0
+        rc = L.jh_qmatvec_batched_swiglu_dev(g.handle, u.handle, P(X), B, P(out), P(sg), P(su), None)
+        assert rc == 0, L.jh_last_error()
+        torch.cuda.synchronize()
+        assert torch.isfinite(ref).all()
+        assert torch.equal(out, ref)
+    finally:
+        g.close()
+        u.close()
