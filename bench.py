@@ -463,12 +463,15 @@ def tinyllama_step(torch, stream, steps):
         dec.x.copy_(x0)  # the step updates the residual stream in place
         dec.enqueue_step(stream)
 
-    def gemvs_only():
+    gate = torch.empty(cfg.intermediate_size, device="cuda")
+    up = torch.empty(cfg.intermediate_size, device="cuda")
+
+    def gemvs_only():  # the step's projections alone (gate and up as a plain group)
         for lw in w.layers:
             m = lw.mats
             dec._group([m["q"], m["k"], m["v"]], [dec.xn] * 3, [dec.q, dec.k, dec.v], ctypes.c_void_p(stream.cuda_stream))
             dec._group([m["o"]], [dec.att], [dec.proj], ctypes.c_void_p(stream.cuda_stream))
-            dec._group([m["gate"], m["up"]], [dec.xn] * 2, [dec.gate, dec.up], ctypes.c_void_p(stream.cuda_stream))
+            dec._group([m["gate"], m["up"]], [dec.xn] * 2, [gate, up], ctypes.c_void_p(stream.cuda_stream))
             dec._group([m["down"]], [dec.hid], [dec.proj], ctypes.c_void_p(stream.cuda_stream))
         dec._group([w.output], [dec.xn], [dec.logits], ctypes.c_void_p(stream.cuda_stream))
 
