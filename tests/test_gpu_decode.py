@@ -91,7 +91,8 @@ def test_rope_kv_append(L, nh, nkv, hd):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,T", [(32, 4, 64, 1), (32, 4, 64, 128), (32, 4, 64, 129), (32, 4, 64, 512),
-                                         (32, 8, 128, 300), (8, 8, 64, 1000), (4, 1, 256, 70)])
+                                         (32, 8, 128, 300), (8, 8, 64, 1000), (4, 1, 256, 70),
+                                         (16, 8, 128, 200), (12, 6, 64, 333), (16, 4, 64, 65), (8, 8, 128, 64)])
 def test_attention(L, nh, nkv, hd, T):
     say("attention", nh, nkv, hd, T)
     max_seq = 1024
@@ -111,7 +112,8 @@ def test_attention(L, nh, nkv, hd, T):
 
 
 @pytest.mark.parametrize("nh,nkv,hd,pos", [(32, 4, 64, 0), (32, 4, 64, 63), (32, 4, 64, 64), (32, 4, 64, 511),
-                                           (32, 8, 128, 200), (4, 1, 256, 70)])
+                                           (32, 8, 128, 200), (4, 1, 256, 70), (16, 8, 64, 65), (8, 8, 128, 511),
+                                           (16, 8, 128, 127)])
 def test_rope_attention_fused(L, nh, nkv, hd, pos):
     """rope of q and k, KV append and gqa in one call == the oracle's three steps."""
     say("rope_attention", nh, nkv, hd, pos)
@@ -136,7 +138,7 @@ def test_rope_attention_fused(L, nh, nkv, hd, pos):
     assert np.array_equal(dq.cpu().numpy(), q)  # q itself is not modified
 
 
-@pytest.mark.parametrize("nh,nkv,hd", [(32, 4, 64), (32, 8, 128)])
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 4, 64), (32, 8, 128), (16, 8, 128), (8, 8, 64)])
 @pytest.mark.parametrize("batch", [2, 8, 12])
 def test_rope_attention_batched(L, nh, nkv, hd, batch):
     """jh_rope_attention_batched_dev: each request at its own position and cache
