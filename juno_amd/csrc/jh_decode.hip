@@ -151,6 +151,7 @@ __device__ __forceinline__ void rope_rot(float &x0, float &x1, float c, float s)
 // chunk length: one position per lane, fewer for wide heads (LDS holds the
 // chunk's K and V)
 __host__ __device__ constexpr int attn_tc(int head_dim) { return head_dim <= 128 ? 64 : 32; }
+constexpr int kAttnSmallTc = 32;  // chunk of the one-round kernel when the grid is small
 
 constexpr int kAttnWaves = 4;  // most waves per workgroup; they share the chunk's K and V
 
@@ -448,12 +449,12 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attn_chunk_hd(
 // The new position's K (roped) and V replace the cache rows in LDS and in the
 // registers and are written to the cache.  Results match attn_chunk_k up to
 // the summation order of p . V.
-template <bool FUSED, int HD, int R>
+template <bool FUSED, int HD, int R, int TC>  // TC: positions per chunk (64, or 32 for a grid of few chunks)
 __global__ __launch_bounds__(256) void attn_chunk_rv(
     const float *__restrict__ q, const float *__restrict__ k_new, const float *__restrict__ v_new,
     float *__restrict__ k_cache, float *__restrict__ v_cache, int n_heads, int n_kv_heads, const int *__restrict__ d_pos,
     int max_seq, float theta, float scale, float *__restrict__ part, const int *__restrict__ d_slot, int n_slots) {
-    constexpr int tc = 64, Q4 = HD / 4, M = Q4 - 1;
+    constexpr int tc = TC, Q4 = HD / 4, M = Q4 - 1;
     constexpr int PH = 256 / Q4;         // row phases of p . V
     constexpr int VJ = tc / PH;          // V rows per thread
     constexpr int KJ = tc * Q4 / 256;    // K float4 per thread
@@ -552,11 +553,12 @@ __global__ __launch_bounds__(256) void attn_chunk_rv(
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // lanes past the chunk's end compute on whatever row they hold and are masked
         const float4 *q4 = reinterpret_cast<const float4 *>(sqr);
-        const float4 *k4 = sk4 + lane * Q4;
+        const int kr = min(lane, tc - 1);  // lanes past the chunk read its last row (masked below)
+        const float4 *k4 = sk4 + kr * Q4;
         float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
         for (int j = 0; j < Q4; j++) {
-            const float4 qq = q4[j], kq = k4[j ^ (lane & M)];
+            const float4 qq = q4[j], kq = k4[j ^ (kr & M)];
             a0 = fmaf(qq.x, kq.x, a0);
             a1 = fmaf(qq.y, kq.y, a1);
             a2 = fmaf(qq.z, kq.z, a2);
@@ -568,7 +570,7 @@ __global__ __launch_bounds__(256) void attn_chunk_rv(
         for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
         const float e = lane < nt ? (float)exp((double)(sc - m)) : 0.f;
         const float l = wave_sum(e);
-        sp[r * tc + lane] = e;  // one weight per position (0 past the chunk's end)
+        if (lane < tc) sp[r * tc + lane] = e;  // one weight per position (0 past the chunk's end)
         if (lane == 0) {
             float *hp = part + ((size_t)h * gridDim.y + c) * (HD + 2);
             hp[0] = m;
@@ -603,14 +605,14 @@ __global__ __launch_bounds__(256) void attn_chunk_rv(
     }
 }
 
-template <int HD, int R>
+template <int HD, int R, int TC>
 constexpr size_t attn_rv_lds() {
-    constexpr int tc = 64, PH = 256 / (HD / 4);
+    constexpr int tc = TC, PH = 256 / (HD / 4);
     constexpr int KR = tc * HD > PH * R * HD ? tc * HD : PH * R * HD;
     return sizeof(float) * (KR + HD + R * HD + R * tc + 4);
 }
 
-__global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ part, int head_dim,
+__global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ part, int head_dim, int tc,
                                                       const int *__restrict__ d_pos, int max_seq, int nchmax,
                                                       float *__restrict__ out) {
     // The chunk maxima and normalisers are loaded by one thread per chunk, all at
@@ -619,7 +621,7 @@ __global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ 
     // sequential one without a memory round trip per chunk.
     __shared__ float wc[1024], wl[1024], wmax[4];
     __shared__ float sL;
-    const int h = blockIdx.x, tc = attn_tc(head_dim), z = blockIdx.y;  // head, request
+    const int h = blockIdx.x, z = blockIdx.y;  // head, request
     const int tid = threadIdx.x;
     d_pos += z;
     part += (size_t)z * gridDim.x * nchmax * (head_dim + 2);
@@ -748,7 +750,8 @@ static bool attn_rv_wanted() {
 static bool attn_v_global(int head_dim, int batch) { return head_dim == 128 && batch >= 8; }
 
 size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq, int batch) {
-    const int nch = (max_seq + attn_tc(head_dim) - 1) / attn_tc(head_dim);
+    const int tc = head_dim <= 128 ? kAttnSmallTc : attn_tc(head_dim);  // the finest chunking the launcher may pick
+    const int nch = (max_seq + tc - 1) / tc;
     return (size_t)batch * n_heads * nch * (head_dim + 2) * sizeof(float);
 }
 
@@ -756,7 +759,12 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
                             int n_heads, int n_kv_heads, int head_dim, const int *d_pos, int max_seq, float theta,
                             bool fused, float *out, void *workspace, hipStream_t s, int batch, const int *d_slot,
                             int n_slots) {
-    const int tc = attn_tc(head_dim), nch = (max_seq + tc - 1) / tc;
+    const int R = n_heads / n_kv_heads;
+    const bool rv = (head_dim == 64 || head_dim == 128) && (R == 1 || R == 2 || R == 4 || R == 8) && attn_rv_wanted();
+    // 32-position chunks when the grid would be small (one request): twice the workgroups, each half the rows
+    const bool small = rv && (size_t)batch * n_kv_heads * ((max_seq + 63) / 64) < 512 &&
+                       (max_seq + kAttnSmallTc - 1) / kAttnSmallTc <= 1024;
+    const int tc = small ? kAttnSmallTc : attn_tc(head_dim), nch = (max_seq + tc - 1) / tc;
     if (nch > 1024) return hipErrorNotSupported;  // combine weights live in a fixed LDS array
     const float scale = (float)(1.0 / sqrt((double)head_dim));
     float *part = static_cast<float *>(workspace);
@@ -781,13 +789,14 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
         return ok;
     }();
     (void)attr;
-    const int R = n_heads / n_kv_heads;
-    if ((head_dim == 64 || head_dim == 128) && (R == 1 || R == 2 || R == 4 || R == 8) && attn_rv_wanted()) {
+    if (rv) {
         // (at most ~40 KB of LDS: within the default dynamic limit)
-#define JH_RV(FU, HD, RR)                                                                                          \
-    attn_chunk_rv<FU, HD, RR><<<grid, 256, attn_rv_lds<HD, RR>(), s>>>(                                             \
+#define JH_RV_T(FU, HD, RR, T)                                                                                     \
+    attn_chunk_rv<FU, HD, RR, T><<<grid, 256, attn_rv_lds<HD, RR, T>(), s>>>(                                       \
         q, FU ? k_new : nullptr, FU ? v_new : nullptr, k_cache, v_cache, n_heads, n_kv_heads, d_pos, max_seq, theta, \
         scale, part, d_slot, n_slots)
+#define JH_RV(FU, HD, RR)                                                                                          \
+    if (small) JH_RV_T(FU, HD, RR, kAttnSmallTc); else JH_RV_T(FU, HD, RR, 64)
 #define JH_RV_R(FU, HD)                                                                                            \
     switch (R) {                                                                                                   \
     case 1: JH_RV(FU, HD, 1); break;                                                                               \
@@ -802,6 +811,7 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
         }
 #undef JH_RV_R
 #undef JH_RV
+#undef JH_RV_T
     } else if (head_dim == 64 || head_dim == 128) {
         // many workgroups (a batch): V is read from the cache, so that a workgroup's LDS holds only K and more of
         // them fit per CU
@@ -834,7 +844,7 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
                                                  d_pos, max_seq, theta, scale, part, d_slot, n_slots);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    attn_combine_k<<<dim3(n_heads, batch), 256, 0, s>>>(part, head_dim, d_pos, max_seq, nch, out);
+    attn_combine_k<<<dim3(n_heads, batch), 256, 0, s>>>(part, head_dim, tc, d_pos, max_seq, nch, out);
     return hipGetLastError();
 }
 
