@@ -525,7 +525,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the GEMV shards by rows; see the sharding note in DESIGN.md).", file=sys.stderr)
+              "(the GEMV would shard by rows, one slice of every matrix per GPU).", file=sys.stderr)
         sys.exit(2)
 
     import torch

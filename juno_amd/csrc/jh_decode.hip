@@ -672,7 +672,7 @@ __global__ __launch_bounds__(256) void silu_mul_k(const float *__restrict__ gate
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i < n) {
         const float g = gate[i];
-        out[i] = g / (1.f + (float)exp(-(double)g)) * up[i];
+        out[i] = silu_times(g, up[i]);
     }
 }
 

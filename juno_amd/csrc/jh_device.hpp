@@ -36,6 +36,9 @@ __device__ __forceinline__ uint4 load_stream16(const uint8_t *p) {
 
 __device__ __forceinline__ float4 load_f4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
+// silu(g) * u with silu's exp in double, cast to float (LlamaTransformerHandler.java:1733-1735, 796-797)
+__device__ __forceinline__ float silu_times(float g, float u) { return g / (1.f + (float)exp(-(double)g)) * u; }
+
 // Sum over the 64 lanes of a wavefront with DPP row operations, then the four
 // 16-lane row totals with readlane.  Every lane returns the full sum.
 __device__ __forceinline__ float wave_sum(float v) {

@@ -474,9 +474,6 @@ struct StagedArgs {
 
 // SwiGLU pairing: virtual row v is row v / 2 of gate (v even) or up (v odd),
 // so that a row group (R even) holds both halves of its outputs.
-__device__ __forceinline__ float silu_times(float g, float u) {
-    return g / (1.f + (float)exp(-(double)g)) * u;  // silu_mul_k's arithmetic
-}
 
 __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
     int p = 0;

@@ -735,10 +735,6 @@ __host__ __device__ constexpr int lds_bytes() {
     return (NT == 1 ? 2 : 1) * lds_w_offset<NT>() + kWaves * kRowsPerWave * max_chunks<MASK>() * 16 + kWinPad;
 }
 
-__device__ __forceinline__ float silu_times(float g, float u) {
-    return g / (1.f + (float)exp(-(double)g)) * u;  // silu_mul_k's arithmetic
-}
-
 // store_tile for a SwiGLU pair workgroup (B <= 32): split partials over virtual
 // rows (gate r, up rows + r) in planes of B x 2 rows, the usual hand-off, then
 // the up waves pass their totals to the gate waves through LDS and those store
