@@ -1196,9 +1196,10 @@ static bool plan_group(int n, const MfmaDesc *d, int B, Plan &p) {
     // One workgroup fits per CU (LDS, VGPRs), so the grid runs in rounds of
     // kMinWorkgroups.  Cost of a split, in super-block steps: rounds x (super-
     // blocks per workgroup + a workgroup's fixed prologue and epilogue, ~5
-    // steps), plus one for the hand-off when K is split; the smallest split
-    // wins ties.  Fitted to the 8B B = 32 shapes ([gate, up]: 2 splits 44 us,
-    // 3 splits 57 us, 16 splits 96 us).
+    // steps), plus one for the hand-off when K is split and a quarter step per
+    // split (the partials the last workgroup sums); the smallest split wins
+    // ties.  Fitted to the 8B B = 32 shapes ([gate, up]: 2 splits 44 us,
+    // 3 splits 57 us, 16 splits 96 us; [o]: 8 splits ahead of 16).
     int best = 1 << 30;
     p.ksb = p.nsb;
     p.ksplit = 1;
@@ -1206,7 +1207,7 @@ static bool plan_group(int n, const MfmaDesc *d, int B, Plan &p) {
         const int ksb = (p.nsb + ks - 1) / ks, kse = (p.nsb + ksb - 1) / ksb;
         if (kse > 1 && tiles > kMaxTileCounters) break;  // a split needs a counter per tile
         const int rounds = (tiles * kse + kMinWorkgroups - 1) / kMinWorkgroups;
-        const int cost = rounds * (ksb + 5) + (kse > 1 ? 1 : 0);
+        const int cost = 4 * (rounds * (ksb + 5) + (kse > 1 ? 1 : 0)) + (kse > 1 ? kse : 0);  // quarter steps
         if (cost < best) {
             best = cost;
             p.ksb = ksb;
