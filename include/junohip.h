@@ -30,6 +30,15 @@
  *     thread has its own HIP stream and staging buffers per device.
  *   - Device-pointer entry points (*_dev) enqueue on the given stream
  *     (NULL = the default stream) and return without synchronising.
+ *   - Some *_dev calls use a library workspace of the stream they are given
+ *     (batched MFMA GEMVs, attention, LoRA, the small-matrix SwiGLU path).
+ *     It is allocated, or grown, only outside graph capture: before capturing
+ *     such calls, make each of them once eagerly on the same stream with the
+ *     same sizes, or the captured call fails with JH_EINVAL.  A workspace that
+ *     grows is replaced, never freed, so graphs captured earlier stay valid.
+ *     A captured graph uses its stream's workspace: do not replay it while
+ *     other work on that workspace (the same stream's calls or another replay)
+ *     is running on another stream.
  */
 #ifndef JUNOHIP_H
 #define JUNOHIP_H
@@ -176,6 +185,21 @@ int jh_qmatvec_batched_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const 
  * projection step of its batched replacement. */
 int jh_qmatvec_batched_group_dev(int n, const jh_qmat *const *mats, const float *const *d_X, int B,
                                  float *const *d_Y, void *stream);
+
+/* Diagnostics: the kernel jh_qmatvec_batched_group_dev takes for these n
+ * matrices (full row ranges) at batch B: *kernel = 0 for the VALU kernels,
+ * 1 for the grouped MFMA kernel with K split *ksplit ways, 2 for the
+ * prepared-x MFMA kernel (one matrix with enough row tiles to fill the GPU
+ * unsplit, B <= 32: the output projection).  No counterpart in the reference;
+ * for tests that must reach a given kernel. */
+int jh_qmatvec_batched_plan(int n, const jh_qmat *const *mats, int B, int *kernel, int *ksplit);
+
+/* Diagnostics of the per-stream library workspace (see Conventions): the
+ * scratch bytes the stream `stream` on `device` currently has (0 before its
+ * first use) and the base address of its live allocation, which changes when
+ * the workspace grows.  No counterpart in the reference; for tests and tools
+ * that check that captured graphs survive growth. */
+int jh_stream_workspace_info(int device, void *stream, size_t *scratch_bytes, void **base);
 
 /* Raw-pointer variant of the quantizer: n fp32 values -> packed bytes in a
  * caller-provided device buffer of rawByteCount(type, n) bytes. */

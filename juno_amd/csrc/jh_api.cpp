@@ -180,55 +180,68 @@ int check_range(const jh_qmat *m, int row_start, int row_end) {
 
 int gemv_path();
 
-// Device workspace of the batched MFMA path, one per (device, stream): work on
-// one stream is ordered, so a stream's launches never overlap in it.  Sized on
-// first use (at least 8 MB) and grown if needed; growth frees the old buffer
-// after a device synchronisation, so size it with an eager call before graph
-// capture.  Released at process exit.
+// Device workspace, one per (device, stream): the MFMA path's prepared x slabs
+// and split-K partials, the attention partials, the LoRA intermediate.  Work
+// on one stream is ordered, so a stream's launches never overlap in it.  One
+// allocation holds the split-K arrival counters (kCounterSlots 128-byte-spaced
+// ints, zeroed on the stream when allocated; every launch leaves them zero)
+// followed by the scratch area.
+//
+// A HIP graph captured from calls on a stream keeps the addresses of that
+// stream's workspace and counters.  So a buffer is never freed while the
+// process runs: when a call needs more scratch than the stream has, a larger
+// buffer (at least twice the old one, with fresh counters) replaces it for
+// later calls, and the old one stays allocated, so that graphs captured
+// earlier still replay into valid memory.  Growth is geometric, so the retired
+// buffers total less than the live one.  Growth cannot happen inside a graph
+// capture (no allocation may be recorded, and the counters' zeroing must not be
+// a graph node): the call then fails and names the eager call to make first.
+// A graph shares its stream's workspace: replaying it on another stream while
+// work that uses the same workspace runs is a race, like any two overlapping
+// launches on one buffer.
+struct Workspace {
+    uint8_t *base = nullptr;  // counters, then scratch
+    size_t cap = 0;           // scratch bytes
+};
+constexpr size_t kCounterBytes = sizeof(int) * (size_t)jh::kCounterSlots * jh::kCounterStride;
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, std::pair<void *, size_t>> g_ws;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
-// Arrival counters of the MFMA split-K hand-off, one block of
-// kCounterSlots 128-byte-spaced counters per (device, stream), zeroed when
-// allocated (so the first use must be eager, like the workspace's); every
-// launch leaves them zero again.
-std::map<std::pair<int, hipStream_t>, int *> g_counters;
-
-int stream_counters(int device, hipStream_t s, int **out) {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    int *&c = g_counters[{device, s}];
-    if (!c) {
-        void *p = nullptr;
-        const size_t bytes = sizeof(int) * (size_t)jh::kCounterSlots * jh::kCounterStride;
-        int rc = device_alloc(&p, bytes);
-        if (rc) return rc;
-        hipError_t e = hipMemset(p, 0, bytes);
-        if (e == hipSuccess) e = hipDeviceSynchronize();
-        if (e != hipSuccess) {
-            (void)hipFree(p);
-            return hip_fail("counter init", e);
-        }
-        c = static_cast<int *>(p);
-    }
-    *out = c;
+int stream_is_capturing(hipStream_t s, bool *capturing) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    JH_HIP("hipStreamIsCapturing", hipStreamIsCapturing(s, &st));
+    *capturing = st != hipStreamCaptureStatusNone;
     return JH_OK;
 }
 
-int stream_workspace(int device, hipStream_t s, size_t bytes, void **out) {
+// Scratch of at least `bytes` and the split-K counters of stream s on `device`.
+int stream_workspace(int device, hipStream_t s, size_t bytes, void **out, int **counters = nullptr) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    auto &e = g_ws[{device, s}];
-    if (e.second < bytes) {
-        if (e.first) {
-            (void)hipDeviceSynchronize();
-            (void)hipFree(e.first);
-            e = {nullptr, 0};
-        }
-        size_t want = bytes < (8u << 20) ? (8u << 20) : bytes;
-        int rc = device_alloc(&e.first, want);
+    Workspace &e = g_ws[{device, s}];
+    if (!e.base || e.cap < bytes) {
+        bool capturing = false;
+        int rc = stream_is_capturing(s, &capturing);
         if (rc) return rc;
-        e.second = want;
+        if (capturing)
+            return fail(JH_EINVAL,
+                        "device workspace of %zu bytes needed during graph capture (stream has %zu): make one eager "
+                        "call of the same size on this stream before capturing",
+                        bytes, e.cap);
+        size_t want = bytes < (8u << 20) ? (8u << 20) : bytes;
+        if (e.base && want < 2 * e.cap) want = 2 * e.cap;
+        void *p = nullptr;
+        if ((rc = device_alloc(&p, kCounterBytes + want))) return rc;
+        hipError_t me = hipMemsetAsync(p, 0, kCounterBytes, s);
+        if (me != hipSuccess) {
+            (void)hipFree(p);  // never handed out
+            return hip_fail("hipMemsetAsync(split-K counters)", me);
+        }
+        // the previous buffer (if any) is retired, not freed: see above
+        e.base = static_cast<uint8_t *>(p);
+        e.cap = want;
     }
-    *out = e.first;
+    *out = e.base + kCounterBytes;
+    if (counters) *counters = reinterpret_cast<int *>(e.base);
     return JH_OK;
 }
 
@@ -242,8 +255,7 @@ int enqueue_mfma_group(int device, int n, const jh::MfmaDesc *d, int B, hipStrea
     if (!wsb) return kMfmaNotApplicable;
     void *ws = nullptr;
     int *counters = nullptr;
-    int rc = stream_workspace(device, s, wsb, &ws);
-    if (!rc) rc = stream_counters(device, s, &counters);
+    int rc = stream_workspace(device, s, wsb, &ws, &counters);
     if (rc) return rc;
     hipError_t e = jh::launch_mfma_group(n, d, B, ws, counters, s);
     if (e == hipSuccess) return JH_OK;
@@ -313,6 +325,31 @@ int set_device(int dev) {
 extern "C" {
 
 const char *jh_last_error(void) { return g_last_error.c_str(); }
+
+int jh_qmatvec_batched_plan(int n, const jh_qmat *const *mats, int B, int *kernel, int *ksplit) {
+    if (n < 1 || n > jh::kMaxMfmaGroup) return fail(JH_EINVAL, "n=%d outside [1, %d]", n, jh::kMaxMfmaGroup);
+    if (!mats || !kernel || !ksplit) return fail(JH_EINVAL, "mats, kernel and ksplit must not be null");
+    jh::MfmaDesc d[jh::kMaxMfmaGroup];
+    int rc;
+    for (int i = 0; i < n; i++) {
+        if ((rc = check_qmat(mats[i]))) return rc;
+        // x is only checked for 16-byte alignment: any aligned stand-in will do
+        d[i] = jh::MfmaDesc{mats[i]->type, mats[i]->d_raw, mats[i]->pitch, mats[i]->cols, 0, mats[i]->rows,
+                            reinterpret_cast<const float *>(mats[i]->d_raw), nullptr};
+    }
+    *ksplit = 1;
+    *kernel = B >= jh::kMfmaMinBatch ? jh::mfma_group_plan(n, d, B, ksplit) : 0;
+    return ok();
+}
+
+int jh_stream_workspace_info(int device, void *stream, size_t *scratch_bytes, void **base) {
+    if (!scratch_bytes || !base) return fail(JH_EINVAL, "scratch_bytes and base must not be null");
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto it = g_ws.find({device, (hipStream_t)stream});
+    *scratch_bytes = it == g_ws.end() ? 0 : it->second.cap;
+    *base = it == g_ws.end() ? nullptr : it->second.base;
+    return ok();
+}
 
 int jh_internal_fail(int code, const char *msg) {
     if (code == JH_OK) return ok();
@@ -649,8 +686,7 @@ int jh_qmatvec_batched_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const 
         const int dev = gate->ctx->device;
         void *ws = nullptr;
         int *counters = nullptr;
-        if ((rc = stream_workspace(dev, s, jh::mfma_swiglu_workspace_bytes(dg, B), &ws))) return rc;
-        if ((rc = stream_counters(dev, s, &counters))) return rc;
+        if ((rc = stream_workspace(dev, s, jh::mfma_swiglu_workspace_bytes(dg, B), &ws, &counters))) return rc;
         hipError_t e = jh::launch_mfma_swiglu(dg, du, B, d_out, ws, counters, s);
         if (e == hipSuccess) return ok();
         if (e != hipErrorNotSupported) return hip_fail("mfma swiglu launch", e);

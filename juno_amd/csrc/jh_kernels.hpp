@@ -82,6 +82,9 @@ constexpr int kMaxMfmaGroup = 4;
 constexpr int kMfmaMinBatch = 3;
 size_t mfma_group_workspace_bytes(int n, const MfmaDesc *d, int B);
 hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, int *counters, hipStream_t s);
+// Which kernel launch_mfma_group takes: 0 none (the path does not apply),
+// 1 mfma_group (K split *ksplit ways), 2 x_prep + mfma_px (one unsplit matrix).
+int mfma_group_plan(int n, const MfmaDesc *d, int B, int *ksplit);
 // out[b][r] = silu(gate_r . x_b) * (up_r . x_b) for 3 <= B <= 32: one MFMA
 // launch whose workgroups take 128 rows of gate and the same 128 rows of up
 // (Q4_K, Q5_K, Q6_K, Q8_0; full row ranges, same shape and x).

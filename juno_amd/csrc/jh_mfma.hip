@@ -9,7 +9,8 @@
 // accumulator of a lane holds one weight row (its own) for 16 batch columns:
 //
 //  * Weights: each format turns its packed integers into exact fp16 integers
-//    (Q4_K: 1024 + ls*q <= 1969 by one 24-bit multiply-add per pair; Q6_K:
+//    (Q4_K: ls*q <= 945 from 1024 + ls*q by one 24-bit multiply-add and one
+//    fp16 subtraction per pair; Q6_K:
 //    u - 32; Q8_0: q) and applies its fp32 scales per row in registers -- Q4_K
 //    once per 256 columns with d and dmin (the min term is one extra MFMA
 //    against per-sub-block sums of x), Q6_K per 16-column sub-block with the
@@ -26,8 +27,9 @@
 //    next super-block's loads are in flight during the current one's math.
 //    When the row tiles are too few to fill the GPU the K range is split
 //    across workgroups; each split writes its partial tile to the workspace
-//    and a small kernel adds the partials in split order (deterministic; no
-//    float atomics).
+//    and bumps the tile's arrival counter, and the split that arrives last
+//    adds all partials in split order into y in the same launch
+//    (deterministic; no float atomics; see store_tile).
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
 
@@ -275,9 +277,12 @@ template <int CH, int RC>
 __device__ __forceinline__ int win_chunk(int j) { return RC == CH ? j : j + (RC - CH) * (j / CH); }
 
 // Q4_K (matVecQ4Kraw, LlamaTransformerHandler.java:1428-1468): w = d*ls*q - dmin*lm.
-// B = 1024 + ls*q (<= 1969, exact), built with one 24-bit multiply-add per
-// pair; 1024 * sum(x) and the min term (one more MFMA: A = [sub-block sums
-// hi | lo], B = [lm | lm]) are removed per super-block with d and dmin.
+// B = ls*q (<= 945, exact), built as fp16 1024 + ls*q by one 24-bit multiply-
+// add per pair into the exponent byte and one packed fp16 subtraction of 1024
+// (exact); the min term (one more MFMA: A = [sub-block sums hi | lo], B =
+// [lm | lm]) is removed per super-block with d and dmin.  Keeping the 1024 in
+// B and subtracting 1024 * sum(x) afterwards would cost fp32 cancellation
+// wherever |x| is large and the row's weights there are small.
 // Q5_K (Q5 = true, matVecQ5Kraw :1525-1576): q has a 5th bit from qh, so
 // ls*q reaches 1953 and 1024 + ls*q would pass fp16's exact integers; B =
 // ls*q is converted instead (v_cvt_f16_u16, exact below 2048).
@@ -317,6 +322,7 @@ struct FmtKQ {
             ls[j + 4] = (int)((byte_of(r.hd.w, j) & 0x0F) | ((byte_of(r.hd.y, j) & 0xC0) >> 2));
             lm[j + 4] = (int)((byte_of(r.hd.w, j) >> 4) | ((byte_of(r.hd.z, j) & 0xC0) >> 2));
         }
+        const half2v k1024 = {(_Float16)1024.f, (_Float16)1024.f};
         f32x16 acc[NT];
 #pragma unroll
         for (int n = 0; n < NT; n++) acc[n] = (f32x16){};
@@ -344,9 +350,12 @@ struct FmtKQ {
                     w[2 * j] = (_Float16)(uint16_t)(v & 0xFFFF);
                     w[2 * j + 1] = (_Float16)(uint16_t)(v >> 16);
                 } else {
+                    // 1024 + ls*q by the exponent byte, then 1024 off in fp16: exact, and
+                    // the MFMA sums stay the size of the weights' own products
                     const uint32_t v = __umul24(pr[j], (uint32_t)ls[s]) + 0x64006400u;
-                    w[2 * j] = __builtin_bit_cast(_Float16, (uint16_t)(v & 0xFFFF));
-                    w[2 * j + 1] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+                    const half2v h = __builtin_bit_cast(half2v, v) - k1024;
+                    w[2 * j] = h[0];
+                    w[2 * j + 1] = h[1];
                 }
             }
             mfma_xw<NT>(c, w, 16 * t + 8 * c.kh, acc);
@@ -363,8 +372,7 @@ struct FmtKQ {
             float S[16], cs[16];
             col_terms<NT>(c, n, S, cs);
 #pragma unroll
-            for (int i = 0; i < 16; i++)
-                tot[n][i] = fmaf(cs[i], fmaf(d, fmaf(Q5 ? 0.f : -1024.f, S[i], acc[n][i]), -dmin * mn[i]), tot[n][i]);
+            for (int i = 0; i < 16; i++) tot[n][i] = fmaf(cs[i], fmaf(d, acc[n][i], -dmin * mn[i]), tot[n][i]);
         }
     }
 };
@@ -1226,6 +1234,13 @@ size_t mfma_group_workspace_bytes(int n, const MfmaDesc *d, int B) {
     if (!plan_group(n, d, B, p)) return 0;
     const size_t bytes = p.slab_bytes + p.part_floats * sizeof(float);
     return bytes > 256 ? bytes : 256;  // nonzero: the MFMA path applies
+}
+
+int mfma_group_plan(int n, const MfmaDesc *d, int B, int *ksplit) {
+    Plan p;
+    if (!plan_group(n, d, B, p)) return 0;
+    *ksplit = p.ksplit;
+    return p.prepared ? 2 : 1;
 }
 
 template <int NT>
