@@ -12,12 +12,13 @@
 //  * Software pipeline.  The next row group's loads are issued into registers
 //    before the current group is computed from the wave's LDS buffer, so HBM
 //    latency is hidden by the dequant math of the group in hand.
-//  * Integer inner product.  x is converted once per workgroup into a 24-bit
-//    integer per element (one scale per 256 columns) held as three byte limbs,
-//    and the weights' integer quants are multiplied with v_dot4 (i8 / u8).
-//    This needs ~1.7 VALU instructions per Q4_K weight instead of ~2.8 for an
-//    fp32 convert+FMA path, which would otherwise bound the kernel below the
-//    HBM roofline.  Block scales (d, dmin, 6-bit / int8 sub-scales) are fp32.
+//  * Integer inner product.  x is converted once per workgroup into a 30-bit
+//    integer per element (one power-of-two scale per quant sub-block) held as
+//    four signed base-256 digits, and the weights' integer quants are
+//    multiplied with v_dot4_i32_i8.  This needs ~1.4 VALU instructions per Q4_K weight
+//    instead of ~2.8 for an fp32 convert+FMA path, which would otherwise bound
+//    the kernel below the HBM roofline.  Block scales (d, dmin, 6-bit / int8
+//    sub-scales) are fp32.
 //  * Persistent workgroups.  x is converted once per workgroup and kept in
 //    registers while the workgroup walks many row groups: with one column
 //    tile the waves share one LDS image of all of x; with 2-4 column tiles
@@ -27,9 +28,10 @@
 //    column tiles over 2 or 4 waves of a workgroup; the partial sums meet in LDS.
 //
 // Numerics: weights are used exactly; the only approximation beyond fp32
-// summation order is rounding x to 24 bits of the maximum over its 256-column
-// block (shared image) or the lane's 64 (Q8_0: 32) columns (error <= 2^-24 *
-// that maximum per element), the size of an fp32 rounding.
+// summation order is rounding x * 2^s to an integer below 2^30 in magnitude,
+// with one s per quant sub-block of x: exact for elements within 2^6 of the
+// sub-block's maximum |x|, within 2^-18 of themselves down to 2^-12 of it,
+// an absolute error of at most 2^-31 of that maximum below.
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
 
@@ -39,23 +41,6 @@ namespace jh {
 namespace {
 
 // --------------------------------------------------------------------------- helpers
-
-__device__ __forceinline__ float wave_max_all(float v) {
-    int x = __builtin_bit_cast(int, v);
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, true)));
-    x = __builtin_bit_cast(int, v);
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true)));
-    x = __builtin_bit_cast(int, v);
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, true)));
-    x = __builtin_bit_cast(int, v);
-    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, true)));
-    x = __builtin_bit_cast(int, v);
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
 
 // Sum over the wavefront with DPP only; the total is valid in lane 63.
 __device__ __forceinline__ float wave_sum_to63(float v) {
@@ -74,17 +59,10 @@ __device__ __forceinline__ float wave_sum_to63(float v) {
     return v;
 }
 
-__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
-}
-
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-__device__ __forceinline__ int udot4(uint32_t a, uint32_t b, int c) {
-    return (int)__builtin_amdgcn_udot4(a, b, (uint32_t)c, false);
-}
 
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -99,18 +77,25 @@ __device__ __forceinline__ uint32_t lds_word(const uint32_t *w, uint32_t sh, int
 
 // --------------------------------------------------------------------------- x preparation
 //
-// Every x element a lane needs becomes a 24-bit integer xi = rint(x / a) with
-// one scale a = max|x| / (2^23 - 1) over a group of columns (the lane's own 64
-// for Q4_K / Q6_K or 32 for Q8_0; a 256-column block in the shared image
-// below), split into three byte limbs
-//   xi = 65536 * hi + 256 * mid + lo,   hi signed, mid and lo unsigned,
-// so that sum(q * x) = a * (65536 * sum(q*hi) + 256 * sum(q*mid) + sum(q*lo))
-// with three v_dot4 products per 4 quants and exact integer sums.  The
-// resolution is 2^-23 of the group's maximum (about fp32's), so the integer
-// path adds no error of consequence to the fp32 accumulation.
+// Every x element a lane needs becomes an integer xi = rint(x * 2^s) with one
+// power-of-two scale 2^-s per scale group: the columns of one quant sub-block
+// of the weight format (G = 32 for Q4_K / Q5_K sub-blocks and Q8_0 blocks, 16
+// for Q6_K sub-blocks).  s puts the group's largest |x| in [2^29, 2^30).
+// Scaling by a power of two is exact, and an element within 2^6 of the maximum
+// is an integer after it (24 significant bits), so such elements are held
+// exactly; an element down to 2^-12 of the maximum is rounded by at most
+// 2^-18 of itself.  xi is held as four balanced base-256 digits
+//   xi = sum_k d_k 256^(3-k),  d_k in [-128, 127],
+// so that sum(q * x) = 2^-s * sum_k 256^(3-k) sum(q * d_k): four signed
+// v_dot4_i32_i8 products per 4 quants with exact integer sums.  Every
+// format's quants enter as signed bytes, so no bias term has to be removed
+// afterwards (a fp32 cancellation when x has an outlier).  Elements below
+// 2^-12 of their sub-block's maximum keep an absolute error of at most 2^-31
+// of that maximum.
+constexpr int kLimbs = 4;
 
 // cols is a multiple of 32: a float4 is either wholly inside or wholly past
-// the end.  The load is clamped in range; to_limbs zeroes the float4s that
+// the end.  The load is clamped in range; the caller zeroes the float4s that
 // lie past the end (at use, so the load is not waited for here).
 __device__ __forceinline__ float4 x_load4(const float *X, int cols, int c) {
     return *reinterpret_cast<const float4 *>(X + min(c, cols - 4));
@@ -121,45 +106,31 @@ __device__ __forceinline__ float4 x_mask4(float4 v, int cols, int c) {
 __device__ __forceinline__ float amax4(float4 v) {
     return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
-constexpr float kMaxInt = 8388607.f;  // 2^23 - 1
+// The shift s of a group with maximum |x| = mx (|x * 2^s| < 2^30), and its
+// scale 2^-s (0 for an all-zero group, so that it contributes nothing).
+__device__ __forceinline__ int x_shift(float mx) { return mx > 0.f ? 30 - __builtin_amdgcn_frexp_expf(mx) : 0; }
+__device__ __forceinline__ float x_scale(float mx, int s) { return mx > 0.f ? ldexpf(1.f, -s) : 0.f; }
 
-// the three limb dwords of 4 consecutive x values (inv = (2^23 - 1) / max)
-__device__ __forceinline__ void to_limbs(float4 v, float inv, uint32_t &h, uint32_t &m, uint32_t &l, int &sm,
-                                         int &sl) {
+// The digit dwords of 4 consecutive x values: dword k holds digit k of value
+// j in byte j (the bytes of xi + 0x80808080, each less 128).
+struct Limbs {
+    uint32_t b[kLimbs];  // b[0]: the top digit (256^3)
+};
+__device__ __forceinline__ Limbs to_limbs(float4 v, int s) {
     const float e[4] = {v.x, v.y, v.z, v.w};
-    h = m = l = 0;
+    Limbs r;
+#pragma unroll
+    for (int k = 0; k < kLimbs; k++) r.b[k] = 0u;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const int xi = max(-8388607, min(8388607, (int)rintf(e[j] * inv)));
-        const uint32_t u = (uint32_t)xi;
-        h |= ((u >> 16) & 0xFFu) << (8 * j);
-        m |= ((u >> 8) & 0xFFu) << (8 * j);
-        l |= (u & 0xFFu) << (8 * j);
-        sm += (int)((u >> 8) & 0xFFu);
-        sl += (int)(u & 0xFFu);
+        const uint32_t u = (uint32_t)(int)rintf(ldexpf(e[j], s)) + 0x80808080u;  // |xi| < 2^30
+#pragma unroll
+        for (int k = 0; k < kLimbs; k++) r.b[k] |= ((u >> (24 - 8 * k)) & 0xFFu) << (8 * j);
     }
+#pragma unroll
+    for (int k = 0; k < kLimbs; k++) r.b[k] ^= 0x80808080u;
+    return r;
 }
-
-// Rows of one column tile (gw == 1) need all of x in every wave of the
-// workgroup: there the waves convert x once, cooperatively, into an LDS image
-// with one scale per 256 columns, and each lane loads its registers from it.
-// LDS image: hi | mid | lo  [cols_pad] int8 each, scale[nblk] f32 (= a),
-// xs16[cols_pad/16] f32 (exact fp32 sums of 16 x), smid32 / slo32
-// [cols_pad/32] i32 (sums of the mid / lo limbs over 32 columns, for the
-// signed Q8_0 quants).  cols_pad = 256 * nblk; columns >= cols read as 0.
-
-struct XImage {
-    int cols, nblk;
-    uint8_t *base;
-    __device__ uint32_t *hi() const { return reinterpret_cast<uint32_t *>(base); }
-    __device__ uint32_t *mid() const { return reinterpret_cast<uint32_t *>(base + 256 * nblk); }
-    __device__ uint32_t *lo() const { return reinterpret_cast<uint32_t *>(base + 512 * nblk); }
-    __device__ float *scale() const { return reinterpret_cast<float *>(base + 768 * nblk); }
-    __device__ float *xs16() const { return scale() + nblk; }
-    __device__ int *smid32() const { return reinterpret_cast<int *>(xs16() + 16 * nblk); }
-    __device__ int *slo32() const { return smid32() + 8 * nblk; }
-    static __host__ __device__ size_t bytes(int nblk) { return (size_t)nblk * (768 + 4 + 64 + 32 + 32); }
-};
 
 // sum of v over the 4 lanes of a quad, in every lane of the quad
 __device__ __forceinline__ float quad_sum(float v) {
@@ -168,107 +139,134 @@ __device__ __forceinline__ float quad_sum(float v) {
     x = __builtin_bit_cast(int, v);
     return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, true));  // 2,3,0,1
 }
-// sum of v over the 8 lanes 8k .. 8k+7, in every one of them
-__device__ __forceinline__ int oct_sum(int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, true);   // quad_perm 1,0,3,2
-    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, true);   // quad_perm 2,3,0,1
-    return v + __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, true);  // row_half_mirror
+// max (MAX) or min of v over the 4 lanes of a quad (G = 16) or the 8 lanes 8k .. 8k+7 (G = 32)
+template <int SEL, bool MAX>
+__device__ __forceinline__ float dpp_red(float v) {
+    const float o = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), SEL, 0xF, 0xF, true));
+    return MAX ? fmaxf(v, o) : fminf(v, o);
+}
+template <int G, bool MAX>
+__device__ __forceinline__ float group_red(float v) {
+    v = dpp_red<0xB1, MAX>(v);                  // quad_perm 1,0,3,2
+    v = dpp_red<0x4E, MAX>(v);                  // quad_perm 2,3,0,1
+    if (G == 32) v = dpp_red<0x141, MAX>(v);   // row_half_mirror
+    return v;
 }
 
+// Rows of one column tile (gw == 1) need all of x in every wave of the
+// workgroup: there the waves convert x once, cooperatively, into an LDS image,
+// and each lane loads its registers from it.  LDS image (cols_pad = 256 nblk):
+//   digit k = 0..3: [cols_pad] bytes each
+//   scale [cols_pad / 16] f32: the scale of the group of columns 16i .. 16i+15
+//   xs16 [cols_pad / 16] f32: fp32 sums of 16 x (the Q4_K / Q5_K min terms)
+// Columns >= cols read as 0.
+struct XImage {
+    int cols, nblk;
+    uint8_t *base;
+    __device__ uint32_t *limb(int k) const { return reinterpret_cast<uint32_t *>(base + 256 * k * nblk); }
+    __device__ float *scale() const { return reinterpret_cast<float *>(base + 256 * kLimbs * nblk); }
+    __device__ float *xs16() const { return scale() + 16 * nblk; }
+    static __host__ __device__ size_t bytes(int nblk) { return (size_t)nblk * (256 * kLimbs + 64 + 64); }
+};
+
+// Block b of 256 columns into the image, one wave: the lane holds columns
+// 256 b + 4 lane .. +4.
+template <int G>
 __device__ __forceinline__ void x_quant_block(const XImage &im, int b, float4 v) {
     const int lane = threadIdx.x & 63;
     if (b * 256 + lane * 4 >= im.cols) v = make_float4(0.f, 0.f, 0.f, 0.f);
-    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    m = wave_max_all(m);
-    const float a = m * (1.f / kMaxInt);
-    const float inv = m > 0.f ? kMaxInt / m : 0.f;
-    const float e[4] = {v.x, v.y, v.z, v.w};
-    uint32_t ph = 0, pm = 0, pl = 0;
-    int sm = 0, sl = 0;
+    const float mx = group_red<G, true>(amax4(v));
+    const int s = x_shift(mx);
+    const Limbs l = to_limbs(v, s);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int xi = max(-8388607, min(8388607, (int)rintf(e[j] * inv)));
-        const uint32_t u = (uint32_t)xi;
-        ph |= ((u >> 16) & 0xFFu) << (8 * j);
-        pm |= ((u >> 8) & 0xFFu) << (8 * j);
-        pl |= (u & 0xFFu) << (8 * j);
-        sm += (int)((u >> 8) & 0xFFu);
-        sl += (int)(u & 0xFFu);
-    }
-    im.hi()[b * 64 + lane] = ph;
-    im.mid()[b * 64 + lane] = pm;
-    im.lo()[b * 64 + lane] = pl;
-    // sums over 4 lanes (16 columns) and 8 lanes (32 columns) with DPP
-    // (quad_perm and row_half_mirror) rather than LDS permutes
-    const float s = quad_sum((v.x + v.y) + (v.z + v.w));
-    if ((lane & 3) == 0) im.xs16()[b * 16 + (lane >> 2)] = s;
-    sm = oct_sum(sm);
-    sl = oct_sum(sl);
-    if ((lane & 7) == 0) {
-        im.smid32()[b * 8 + (lane >> 3)] = sm;
-        im.slo32()[b * 8 + (lane >> 3)] = sl;
-    }
-    if (lane == 0) im.scale()[b] = a;
+    for (int k = 0; k < kLimbs; k++) im.limb(k)[b * 64 + lane] = l.b[k];
+    if ((lane & 3) == 0) im.scale()[b * 16 + (lane >> 2)] = x_scale(mx, s);  // per 16 columns (G = 32: twice)
+    // sums over 4 lanes (16 columns) with DPP (quad_perm) rather than LDS permutes
+    const float xs = quad_sum((v.x + v.y) + (v.z + v.w));
+    if ((lane & 3) == 0) im.xs16()[b * 16 + (lane >> 2)] = xs;
 }
 
-// 65536*h + 256*m + l of three dot-product partial sums, in fp32.
-__device__ __forceinline__ float limbs(int h, int m, int l) {
-    return fmaf((float)h, 65536.f, fmaf((float)m, 256.f, (float)l));
+// sum_k 256^(3-k) h_k of the four digit dot products, in fp32: two exact
+// int32 partial sums (|h_k| <= 32 * 128 * 128), so only their conversions
+// and the add round.
+__device__ __forceinline__ float limbs(const int (&h)[kLimbs]) {
+    const int top = (h[0] << 8) + h[1], low = (h[2] << 8) + h[3];
+    return fmaf((float)top, 65536.f, (float)low);
 }
 
 // --------------------------------------------------------------------------- formats
 
 // Per-format constants: block quant count, block bytes, lanes per block, max
-// blocks per wave tile, max 16-byte chunks of one row tile in LDS.
+// blocks per wave tile, max 16-byte chunks of one row tile in LDS, x scale group.
 template <int T> struct Fmt;
-template <> struct Fmt<12> { static constexpr int QK = 256, BB = 144, LPB = 4, TBMAX = 16, CH = 145; };
-template <> struct Fmt<13> { static constexpr int QK = 256, BB = 176, LPB = 4, TBMAX = 16, CH = 177; };
-template <> struct Fmt<14> { static constexpr int QK = 256, BB = 210, LPB = 4, TBMAX = 16, CH = 212; };
-template <> struct Fmt<8> { static constexpr int QK = 32, BB = 34, LPB = 1, TBMAX = 64, CH = 138; };
+template <> struct Fmt<12> { static constexpr int QK = 256, BB = 144, LPB = 4, TBMAX = 16, CH = 145, G = 32; };
+template <> struct Fmt<13> { static constexpr int QK = 256, BB = 176, LPB = 4, TBMAX = 16, CH = 177, G = 32; };
+template <> struct Fmt<14> { static constexpr int QK = 256, BB = 210, LPB = 4, TBMAX = 16, CH = 212, G = 16; };
+template <> struct Fmt<8> { static constexpr int QK = 32, BB = 34, LPB = 1, TBMAX = 64, CH = 138, G = 32; };
 
-// x registers a lane keeps for its block slot: N dwords per limb.
+// x registers a lane keeps for its block slot: N dwords per digit.
 template <int N> struct XLimbs {
-    uint32_t h[N], m[N], l[N];
+    uint32_t b[kLimbs][N];
     __device__ void load_run(const XImage &im, int dw, int at, int n) {  // n dwords from dword index dw
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            if (k >= n / 4) break;
-            const uint4 t = *reinterpret_cast<const uint4 *>(im.hi() + dw + 4 * k);
-            h[at + 4 * k] = t.x; h[at + 4 * k + 1] = t.y; h[at + 4 * k + 2] = t.z; h[at + 4 * k + 3] = t.w;
-            const uint4 u = *reinterpret_cast<const uint4 *>(im.mid() + dw + 4 * k);
-            m[at + 4 * k] = u.x; m[at + 4 * k + 1] = u.y; m[at + 4 * k + 2] = u.z; m[at + 4 * k + 3] = u.w;
-            const uint4 w = *reinterpret_cast<const uint4 *>(im.lo() + dw + 4 * k);
-            l[at + 4 * k] = w.x; l[at + 4 * k + 1] = w.y; l[at + 4 * k + 2] = w.z; l[at + 4 * k + 3] = w.w;
-        }
+        for (int k = 0; k < kLimbs; k++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                if (r >= n / 4) break;
+                const uint4 t = *reinterpret_cast<const uint4 *>(im.limb(k) + dw + 4 * r);
+                b[k][at + 4 * r] = t.x; b[k][at + 4 * r + 1] = t.y; b[k][at + 4 * r + 2] = t.z; b[k][at + 4 * r + 3] = t.w;
+            }
+    }
+    __device__ void set(int i, const Limbs &l) {
+#pragma unroll
+        for (int k = 0; k < kLimbs; k++) b[k][i] = l.b[k];
+    }
+    // the digit dot products of 4 quants (signed bytes) with x dword i
+    __device__ __forceinline__ void dot(uint32_t q, int i, int (&h)[kLimbs]) const {
+#pragma unroll
+        for (int k = 0; k < kLimbs; k++) h[k] = sdot4(q, b[k][i], h[k]);
     }
 };
+
+// Per-lane conversion (column tiles, no shared image): the group's digit
+// dwords for n float4s v[0..n) starting at register index at, and its scale.
+template <int N, int M>
+__device__ __forceinline__ float convert_group(XLimbs<N> &x, const float4 (&v)[M], int at, int n) {
+    float mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < M; k++)
+        if (k >= at && k < at + n) mx = fmaxf(mx, amax4(v[k]));
+    const int s = x_shift(mx);
+#pragma unroll
+    for (int k = 0; k < M; k++)
+        if (k >= at && k < at + n) x.set(k, to_limbs(v[k], s));
+    return x_scale(mx, s);
+}
 
 template <int T> struct XRegs;
 
 // Q4_K: 64 columns b*256 + 64g .. +64, i.e. sub-blocks 2g ([0..7]) and 2g+1 ([8..15])
 template <> struct XRegs<12> : XLimbs<16> {
-    float a, xs0, xs1;
+    float a0, a1, xs0, xs1;
     static __device__ __forceinline__ int col(int b, int g, int k) { return b * 256 + 64 * g + 4 * k; }
     __device__ void load(const XImage &im, int b, int g, bool act) {
         load_run(im, (b * 256 + 64 * g) / 4, 0, 16);
         const float4 s = *reinterpret_cast<const float4 *>(im.xs16() + b * 16 + 4 * g);
-        a = act ? im.scale()[b] : 0.f;
+        a0 = act ? im.scale()[b * 16 + 4 * g] : 0.f;
+        a1 = act ? im.scale()[b * 16 + 4 * g + 2] : 0.f;
         xs0 = act ? s.x + s.y : 0.f;
         xs1 = act ? s.z + s.w : 0.f;
     }
     __device__ void convert(const float4 (&v)[16], bool act) {
-        float mx = 0.f, s0 = 0.f, s1 = 0.f;
+        float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            mx = fmaxf(mx, amax4(v[k]));
             const float s = (v[k].x + v[k].y) + (v[k].z + v[k].w);
             if (k < 8) s0 += s; else s1 += s;
         }
-        const float inv = mx > 0.f ? kMaxInt / mx : 0.f;
-        int sm = 0, sl = 0;
-#pragma unroll
-        for (int k = 0; k < 16; k++) to_limbs(v[k], inv, h[k], m[k], l[k], sm, sl);
-        a = act ? mx * (1.f / kMaxInt) : 0.f;
+        const float c0 = convert_group(*this, v, 0, 8), c1 = convert_group(*this, v, 8, 8);
+        a0 = act ? c0 : 0.f;
+        a1 = act ? c1 : 0.f;
         xs0 = act ? s0 : 0.f;
         xs1 = act ? s1 : 0.f;
     }
@@ -277,9 +275,10 @@ template <> struct XRegs<12> : XLimbs<16> {
 // Q5_K: the same columns as Q4_K
 template <> struct XRegs<13> : XRegs<12> {};
 
-// Q6_K: runs k = 0..3 of 16 columns b*256 + hh*128 + 32k + l0 (hh = g/2, l0 = 16(g&1))
+// Q6_K: runs r = 0..3 of 16 columns b*256 + hh*128 + 32r + l0 (hh = g/2, l0 = 16(g&1)),
+// each one Q6_K sub-block with its own x scale
 template <> struct XRegs<14> : XLimbs<16> {
-    float a, m32[4];
+    float a[4];
     static __device__ __forceinline__ int col(int b, int g, int k) {
         return b * 256 + (g >> 1) * 128 + 32 * (k >> 2) + 16 * (g & 1) + 4 * (k & 3);
     }
@@ -289,47 +288,29 @@ template <> struct XRegs<14> : XLimbs<16> {
         for (int k = 0; k < 4; k++) {
             const int c = b * 256 + hh * 128 + 32 * k + l0;
             load_run(im, c / 4, 4 * k, 4);
-            m32[k] = act ? -32.f * im.xs16()[c / 16] : 0.f;
+            a[k] = act ? im.scale()[c / 16] : 0.f;
         }
-        a = act ? im.scale()[b] : 0.f;
     }
     __device__ void convert(const float4 (&v)[16], bool act) {
-        float mx = 0.f, s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            mx = fmaxf(mx, amax4(v[k]));
-            s[k >> 2] += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+        for (int r = 0; r < 4; r++) {
+            const float c = convert_group(*this, v, 4 * r, 4);
+            a[r] = act ? c : 0.f;
         }
-        const float inv = mx > 0.f ? kMaxInt / mx : 0.f;
-        int sm = 0, sl = 0;
-#pragma unroll
-        for (int k = 0; k < 16; k++) to_limbs(v[k], inv, h[k], m[k], l[k], sm, sl);
-        a = act ? mx * (1.f / kMaxInt) : 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; r++) m32[r] = act ? -32.f * s[r] : 0.f;
     }
 };
 
 // Q8_0: the 32 columns of block b
 template <> struct XRegs<8> : XLimbs<8> {
     float a;
-    int sm, sl;  // limb sums, for the +128 bias of the signed quants
     static __device__ __forceinline__ int col(int b, int, int k) { return b * 32 + 4 * k; }
     __device__ void load(const XImage &im, int b, int, bool act) {
         load_run(im, b * 8, 0, 8);
-        a = act ? im.scale()[b / 8] : 0.f;
-        sm = im.smid32()[b];
-        sl = im.slo32()[b];
+        a = act ? im.scale()[b * 2] : 0.f;
     }
     __device__ void convert(const float4 (&v)[8], bool act) {
-        float mx = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; k++) mx = fmaxf(mx, amax4(v[k]));
-        const float inv = mx > 0.f ? kMaxInt / mx : 0.f;
-        sm = sl = 0;
-#pragma unroll
-        for (int k = 0; k < 8; k++) to_limbs(v[k], inv, h[k], m[k], l[k], sm, sl);
-        a = act ? mx * (1.f / kMaxInt) : 0.f;
+        const float c = convert_group(*this, v, 0, 8);
+        a = act ? c : 0.f;
     }
 };
 
@@ -339,9 +320,8 @@ template <> struct XRegs<8> : XLimbs<8> {
 // Q5_K (Q5 = true, :1525-1576): the same with qs at +48 and q's 5th bit from
 // qh (+16): bit 2g / 2g+1 of qh[l].
 template <bool Q5>
-__device__ __forceinline__ float kq_block_dot(const XRegs<12> &x, const uint8_t *p, int g) {
+__device__ __forceinline__ void kq_quants(const uint8_t *p, int g, uint32_t (&lo)[8], uint32_t (&hi)[8]) {
     constexpr int kQs = Q5 ? 48 : 16;
-    const uint4 hd = *reinterpret_cast<const uint4 *>(p);
     const uint4 qa = *reinterpret_cast<const uint4 *>(p + kQs + 32 * g);
     const uint4 qb = *reinterpret_cast<const uint4 *>(p + kQs + 16 + 32 * g);
     const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
@@ -353,21 +333,31 @@ __device__ __forceinline__ float kq_block_dot(const XRegs<12> &x, const uint8_t 
 #pragma unroll
         for (int k = 0; k < 8; k++) q5[k] = h[k] >> (2 * g);
     }
-    int h0 = 0, m0 = 0, l0 = 0, h1 = 0, m1 = 0, l1 = 0;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        uint32_t lo = q[k] & 0x0F0F0F0Fu, hi = (q[k] >> 4) & 0x0F0F0F0Fu;
+        lo[k] = q[k] & 0x0F0F0F0Fu;
+        hi[k] = (q[k] >> 4) & 0x0F0F0F0Fu;
         if (Q5) {
-            lo |= (q5[k] & 0x01010101u) << 4;
-            hi |= ((q5[k] >> 1) & 0x01010101u) << 4;
+            lo[k] |= (q5[k] & 0x01010101u) << 4;
+            hi[k] |= ((q5[k] >> 1) & 0x01010101u) << 4;
         }
-        h0 = sdot4(lo, x.h[k], h0);
-        m0 = udot4(lo, x.m[k], m0);
-        l0 = udot4(lo, x.l[k], l0);
-        h1 = sdot4(hi, x.h[8 + k], h1);
-        m1 = udot4(hi, x.m[8 + k], m1);
-        l1 = udot4(hi, x.l[8 + k], l1);
     }
+}
+
+template <bool Q5>
+__device__ __forceinline__ float kq_block_dot(const XRegs<12> &x, const uint8_t *p, int g) {
+    const uint4 hd = *reinterpret_cast<const uint4 *>(p);
+    int d0[kLimbs] = {}, d1[kLimbs] = {};
+    {
+        uint32_t lo[8], hi[8];
+        kq_quants<Q5>(p, g, lo, hi);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            x.dot(lo[k], k, d0);  // quants 0..31: non-negative signed bytes
+            x.dot(hi[k], 8 + k, d1);
+        }
+    }
+    const float s0 = x.a0 * limbs(d0), s1 = x.a1 * limbs(d1);
     // 6-bit scale / min of sub-blocks j = 2g, 2g+1 (q4kScaleRaw / q4kMinRaw,
     // LlamaTransformerHandler.java:1471-1482), branch-free: for g >= 2 the low
     // 4 bits come from bytes 8..11 and the top 2 bits from bytes 0..7.
@@ -378,10 +368,10 @@ __device__ __forceinline__ float kq_block_dot(const XRegs<12> &x, const uint8_t 
     const int ls1 = (int)(__builtin_amdgcn_ubfe(wls, 8 * jj + 8, wl) | (__builtin_amdgcn_ubfe(hd.y, 8 * jj + 14, wh) << 4));
     const int lm0 = (int)(__builtin_amdgcn_ubfe(wlm, 8 * jj + mo, wl) | (__builtin_amdgcn_ubfe(hd.z, 8 * jj + 6, wh) << 4));
     const int lm1 = (int)(__builtin_amdgcn_ubfe(wlm, 8 * jj + 8 + mo, wl) | (__builtin_amdgcn_ubfe(hd.z, 8 * jj + 14, wh) << 4));
-    const float t = fmaf((float)ls1, limbs(h1, m1, l1), (float)ls0 * limbs(h0, m0, l0));
+    const float t = fmaf((float)ls1, s1, (float)ls0 * s0);
     const float mn = fmaf((float)lm1, x.xs1, (float)lm0 * x.xs0);
     const float d = half_bits_to_float(hd.x), dmin = half_bits_to_float(hd.x >> 16);
-    return fmaf(d * x.a, t, -dmin * mn);
+    return fmaf(d, t, -dmin * mn);
 }
 __device__ __forceinline__ float block_dot(const XRegs<12> &x, const uint8_t *p, int g) {
     return kq_block_dot<false>(x, p, g);
@@ -390,9 +380,27 @@ __device__ __forceinline__ float block_dot(const XRegs<13> &x, const uint8_t *p,
     return kq_block_dot<true>(x, p, g);
 }
 
+// Q6_K quants as signed bytes 4 * (u - 32), u = (ql nibble) | (2 qh bits) << 4:
+// 4u = (nibble << 2) | (qh bits << 6) fits a byte, and 4u - 128 is 4u with its
+// top bit flipped.  The factor 4 leaves the scale once per run (exact).  The
+// qh word arrives with bit 1 of every 2-bit field flipped (e ^ 0xAAAAAAAA), so
+// each quad is the nibbles (bits 2..5 of each byte) or-ed with the qh bits
+// (bits 6..7).
+__device__ __forceinline__ uint32_t q6_insert(uint32_t nib, uint32_t hb) {
+    return (nib & 0x3C3C3C3Cu) | (hb & 0xC0C0C0C0u);
+}
+// quads 0..3 of dword k of a lane's Q6_K run (ql words a, b; qh word e)
+__device__ __forceinline__ void q6_quads(uint32_t a, uint32_t b, uint32_t e, uint32_t (&q)[4]) {
+    const uint32_t f = e ^ 0xAAAAAAAAu;
+    q[0] = q6_insert(a << 2, f << 6);
+    q[1] = q6_insert(b << 2, f << 4);
+    q[2] = q6_insert(a >> 2, f << 2);
+    q[3] = q6_insert(b >> 2, f);
+}
+
 // Q6_K (LlamaTransformerHandler.java:1587-1638): lane g covers half hh = g/2 and
 // l in [l0, l0+16), l0 = 16*(g&1), for the four quads k (elements l + 32k).
-// q = u - 32 with u = (ql nibble) | (2 qh bits) << 4; scale d * sc[hh*8 + (g&1) + 2k].
+// q = u - 32; scale d * sc[hh*8 + (g&1) + 2k].
 __device__ __forceinline__ float block_dot(const XRegs<14> &x, const uint8_t *p, int g) {
     const int hh = g >> 1, l0 = 16 * (g & 1);
     const uintptr_t pa = reinterpret_cast<uintptr_t>(p);
@@ -403,54 +411,43 @@ __device__ __forceinline__ float block_dot(const XRegs<14> &x, const uint8_t *p,
     const uint32_t *wq = w + (128 + hh * 32 + l0) / 4;
     const uint32_t *ws = w + (192 + hh * 8) / 4;
     const uint32_t *wd = w + 208 / 4;
-    int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+    int acc[4][kLimbs] = {};  // [quad j][digit]
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        const uint32_t a = lds_word(wa, sh, k), b = lds_word(wb, sh, k), e = lds_word(wq, sh, k);
-        const uint32_t u[4] = {(a & 0x0F0F0F0Fu) | ((e << 4) & 0x30303030u),
-                               (b & 0x0F0F0F0Fu) | ((e << 2) & 0x30303030u),
-                               ((a >> 4) & 0x0F0F0F0Fu) | (e & 0x30303030u),
-                               ((b >> 4) & 0x0F0F0F0Fu) | ((e >> 2) & 0x30303030u)};
+        uint32_t q[4];
+        q6_quads(lds_word(wa, sh, k), lds_word(wb, sh, k), lds_word(wq, sh, k), q);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            ah[j] = sdot4(u[j], x.h[4 * j + k], ah[j]);
-            am[j] = udot4(u[j], x.m[4 * j + k], am[j]);
-            al[j] = udot4(u[j], x.l[4 * j + k], al[j]);
-        }
+        for (int j = 0; j < 4; j++) x.dot(q[j], 4 * j + k, acc[j]);
     }
+    float sj[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) sj[j] = x.a[j] * limbs(acc[j]);
     const uint32_t s0 = lds_word(ws, sh, 0), s1 = lds_word(ws, sh, 1);
     const uint32_t dword = lds_word(wd, sh, 0);
     const int is = g & 1;
-    float acc = 0.f;
+    float r = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int idx = is + 2 * j;  // 0..7 within this half's 8 scale bytes
         const int sc = (int)(int8_t)byte_of(idx < 4 ? s0 : s1, idx & 3);
-        acc = fmaf((float)sc, fmaf(x.a, limbs(ah[j], am[j], al[j]), x.m32[j]), acc);
+        r = fmaf((float)sc, sj[j], r);
     }
-    return half_bits_to_float(dword) * acc;
+    return 0.25f * half_bits_to_float(dword) * r;
 }
 
 // Q8_0 (LlamaTransformerHandler.java:1486-1508): one lane per 34-byte block.
-// The signed quants enter the unsigned mid / lo products as q + 128.
 __device__ __forceinline__ float block_dot(const XRegs<8> &x, const uint8_t *p, int) {
     const uintptr_t pa = reinterpret_cast<uintptr_t>(p);
     const uint32_t sh = (uint32_t)(pa & 3u);
     const uint32_t *w = reinterpret_cast<const uint32_t *>(p - sh);
     const float d = half_bits_to_float(lds_word(w, sh, 0));
-    int h = 0, m = 0, l = 0;
+    // quants start 2 bytes into the block
+    auto quants = [&](int k) { return __builtin_amdgcn_alignbyte(w[k + 1 + (sh >> 1)], w[k + (sh >> 1)], (sh + 2) & 3); };
+    int h[kLimbs] = {};
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        // quants start 2 bytes into the block
-        const uint32_t q = __builtin_amdgcn_alignbyte(w[k + 1 + (sh >> 1)], w[k + (sh >> 1)], (sh + 2) & 3);
-        const uint32_t qb = q ^ 0x80808080u;
-        h = sdot4(q, x.h[k], h);
-        m = udot4(qb, x.m[k], m);
-        l = udot4(qb, x.l[k], l);
-    }
-    m -= 128 * x.sm;
-    l -= 128 * x.sl;
-    return d * x.a * limbs(h, m, l);
+    for (int k = 0; k < 8; k++) x.dot(quants(k), k, h);
+    const float s = x.a * limbs(h);
+    return d * s;
 }
 
 // --------------------------------------------------------------------------- kernel
@@ -484,7 +481,7 @@ __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
 }
 
 template <int T, int R, bool SX>  // SX: one column tile, x shared through an LDS image
-__global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
+__device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     using F = Fmt<T>;
     constexpr int K = (F::CH + 63) / 64;  // 16-byte loads per lane per row
     extern __shared__ __align__(16) uint8_t lds[];
@@ -566,9 +563,9 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
     if constexpr (shared_x) {
 #pragma unroll
         for (int k = 0; k < 4; k++)
-            if (wave + 4 * k < nblk) x_quant_block(im, wave + 4 * k, xv[k]);
+            if (wave + 4 * k < nblk) x_quant_block<F::G>(im, wave + 4 * k, xv[k]);
         for (int bx = wave + 16; bx < nblk; bx += 4)
-            x_quant_block(im, bx, x_load4(args.x, args.cols, bx * 256 + lane * 4));
+            x_quant_block<F::G>(im, bx, x_load4(args.x, args.cols, bx * 256 + lane * 4));
         __syncthreads();
         xr.load(im, b, sub, act);
     } else {
@@ -649,14 +646,57 @@ __global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
 }
 
 template <int T, int R, bool SX>
-hipError_t launch_staged_sx(const StagedArgs &sa, size_t lds, int wgs, hipStream_t s) {
+__global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
+    gemv_staged_body<T, R, SX>(args);
+}
+// the same kernel held to 168 VGPRs (three waves per SIMD)
+template <int T, int R, bool SX>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemv_staged_w3(StagedArgs args) {
+    gemv_staged_body<T, R, SX>(args);
+}
+
+static int staged_occupancy() {
+    static const int o = [] {
+        const char *v = getenv("JUNO_STAGED_W3");
+        return v ? atoi(v) : 0;
+    }();
+    return o;
+}
+
+// Workgroups of `kern` with `lds` bytes of dynamic LDS that fit on the device
+// at once (at most 3 per CU).
+static int resident_workgroups(const void *kern, size_t lds) {
+    static int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+            n = 256;
+        return n;
+    }();
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    return cus * (per_cu > 3 ? 3 : per_cu);
+}
+
+template <int T, int R, bool SX>
+hipError_t launch_staged_sx(const StagedArgs &sa, size_t lds, int need, hipStream_t s) {
     static bool attr_set = [] {
         // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950)
         return hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_staged<T, R, SX>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess &&
+               hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_staged_w3<T, R, SX>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
     }();
     (void)attr_set;
-    gemv_staged<T, R, SX><<<wgs, 256, lds, s>>>(sa);
+    const void *kern = staged_occupancy() ? reinterpret_cast<const void *>(&gemv_staged_w3<T, R, SX>)
+                                          : reinterpret_cast<const void *>(&gemv_staged<T, R, SX>);
+    // persistent grid: as many workgroups as fit at once, capped by the work
+    int wgs = resident_workgroups(kern, lds);
+    if (wgs > need) wgs = need;
+    if (staged_occupancy())
+        gemv_staged_w3<T, R, SX><<<wgs, 256, lds, s>>>(sa);
+    else
+        gemv_staged<T, R, SX><<<wgs, 256, lds, s>>>(sa);
     return hipGetLastError();
 }
 
@@ -671,13 +711,8 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
                        2 * 4 * R * 4;
     const int slots = 4 / sa.gw;
     const int ngroups = (sa.nrows + R - 1) / R;
-    // persistent grid: as many workgroups as fit at once, capped by the work
-    int per_cu = (int)(160 * 1024 / lds);
-    per_cu = per_cu < 1 ? 1 : (per_cu > 3 ? 3 : per_cu);
-    int wgs = 256 * per_cu;
     const int need = (ngroups + slots - 1) / slots;
-    if (wgs > need) wgs = need;
-    return sa.gw == 1 ? launch_staged_sx<T, R, true>(sa, lds, wgs, s) : launch_staged_sx<T, R, false>(sa, lds, wgs, s);
+    return sa.gw == 1 ? launch_staged_sx<T, R, true>(sa, lds, need, s) : launch_staged_sx<T, R, false>(sa, lds, need, s);
 }
 
 }  // namespace
