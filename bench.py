@@ -175,12 +175,18 @@ def dominant_kernel(torch, L, mats, stream, reps):
         xp = (ctypes.c_void_p * 2)(x.data_ptr(), x.data_ptr())
         yp = (ctypes.c_void_p * 2)(ys[0].data_ptr(), ys[1].data_ptr())
         args.append((hs, xp, yp))
+    def launch():
+        for hs, xp, yp in args:
+            if L.jh_qmatvec_group_dev(2, hs, xp, yp, s):
+                raise RuntimeError(L.jh_last_error().decode())
+
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
+        launch()  # eager pass first: validates the arguments outside the capture
+        stream.synchronize()
         with torch.cuda.graph(g, stream=stream):
-            for hs, xp, yp in args:
-                L.jh_qmatvec_group_dev(2, hs, xp, yp, s)
+            launch()
         g.replay()
         stream.synchronize()
         e0.record(stream)
@@ -209,12 +215,44 @@ def d2h_packed(torch, dev):
     return src.cpu().numpy()
 
 
+def host_cpus():
+    """Threads the reference's CPU path would use on this host, and the CPU
+    model.  matVecQ4Kraw runs its rows on IntStream.parallel(), i.e.
+    ForkJoinPool.commonPool() (availableProcessors - 1 workers) plus the
+    calling thread (LlamaTransformerHandler.java:1436): availableProcessors
+    threads.  The JVM's availableProcessors is the CPUs this process may run
+    on (what `nproc` prints), limited by a cgroup CPU quota when one is set."""
+    nproc = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = max(1, -(-int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return nproc, quota, model
+
+
 def cpu_baseline(torch, mats, budget_s):
-    """CPU oracle (C restatement of the Java path) on layer 0's seven GEMVs."""
+    """CPU oracle (C restatement of the Java path) on layer 0's seven GEMVs,
+    on as many threads as the JVM's common pool plus the caller would use."""
     import numpy as np
 
     import oracle
-    threads = min(os.cpu_count() or 1, 16)
+    nproc, quota, model = host_cpus()
+    # Without a cgroup quota, the pool stays within the 16 host CPUs a one-GPU
+    # box grants per GPU (more would time-share the cores of other jobs).
+    threads = min(nproc, quota) if quota else min(nproc, 16)
     layer0 = [m for m in mats if m[0].startswith("blk.0.")]
     host = []
     for name, rows, cols, t, dev in layer0:
@@ -232,8 +270,10 @@ def cpu_baseline(torch, mats, budget_s):
     dt = time.perf_counter() - t0
     gbs = layer_bytes * reps / dt / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"C restatement of Juno's Java matVecQ4Kraw/matVecQ6Kraw (oracle/juno_oracle.c, "
-                      f"-O2 -ffp-contract=off, one task per row) on layer 0's 7 GEMVs "
+            "nproc": nproc, "cgroup_cpu_quota": quota, "cpu_model": model,
+            "sample": f"C++ restatement of Juno's Java CPU path: matVecQ4Kraw/matVecQ6Kraw as restated in "
+                      f"oracle/juno_oracle.c (-O2 -ffp-contract=off, one task per row on {threads} threads, "
+                      f"like ForkJoinPool.commonPool() plus the caller) on layer 0's 7 GEMVs "
                       f"({layer_bytes / 1e6:.1f} MB), {reps} reps in {dt:.1f} s",
             "tok_s_equiv": round(gbs * 1e9 / step_bytes(1), 4)}
 
@@ -368,6 +408,49 @@ def profile_mode(torch, L, be):
     per_launch = 2 * packed_bytes(FFN, HIDDEN, Q4_K) + 4 * (HIDDEN + 2 * FFN)
     print(json.dumps({"profile": "gemv_staged Q4_K [gate, up]", "launches": 32,
                       "algorithmic_bytes_per_launch": per_launch,
+                      "calibration": "torch.mul 2^28 fp32: reads 1073741824 B, writes 1073741824 B"}), flush=True)
+
+
+def profile_mfma_mode(torch, L, be):
+    """Launches for MFMA counter runs (rocprofv3 --pmc): 8 layers' grouped
+    Q4_K [gate, up] GEMVs at B = 32 (mfma_group<1, 1>) and at B = 64
+    (mfma_group<2, 1>), eagerly, 4 times each, then the calibration copy."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0)
+    mats = []
+    for layer in range(8):
+        pair = []
+        for name in ("ffn_gate", "ffn_up"):
+            w = torch.randn(FFN * HIDDEN, generator=g, device="cuda").mul_(0.02)
+            pair.append(be.quantize_dev(Q4_K, w.data_ptr(), FFN, HIDDEN, torch.cuda.current_stream().cuda_stream))
+            del w
+        mats.append(pair)
+    torch.cuda.synchronize()
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {}
+    for B in (32, 64):
+        x = torch.randn(B, HIDDEN, device="cuda")
+        ys = [torch.empty(B, FFN, device="cuda") for _ in range(2)]
+        for _ in range(4):
+            for ga, ua in mats:
+                hs = (ctypes.c_void_p * 2)(ga.handle, ua.handle)
+                xp = (ctypes.c_void_p * 2)(x.data_ptr(), x.data_ptr())
+                yp = (ctypes.c_void_p * 2)(ys[0].data_ptr(), ys[1].data_ptr())
+                if L.jh_qmatvec_batched_group_dev(2, hs, xp, B, yp, s):
+                    raise RuntimeError(L.jh_last_error().decode())
+        torch.cuda.synchronize()
+        kernel, ksplit = ctypes.c_int(), ctypes.c_int()
+        hs = (ctypes.c_void_p * 2)(mats[0][0].handle, mats[0][1].handle)
+        L.jh_qmatvec_batched_plan(2, hs, B, ctypes.byref(kernel), ctypes.byref(ksplit))
+        out[f"b{B}"] = {"launches": 32, "ksplit": ksplit.value, "algorithmic_flops_per_launch": 2 * B * 2 * FFN * HIDDEN,
+                        "issued_f16_mfma_flops_per_launch": 2 * 2 * B * 2 * FFN * HIDDEN,
+                        "algorithmic_bytes_per_launch": 2 * packed_bytes(FFN, HIDDEN, Q4_K) + 4 * B * (HIDDEN + 2 * FFN)}
+    a = torch.empty(1 << 28, device="cuda")
+    a.fill_(1.0)
+    b = torch.empty_like(a)
+    torch.mul(a, 2.0, out=b)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "mfma_group Q4_K [gate, up]", **out,
                       "calibration": "torch.mul 2^28 fp32: reads 1073741824 B, writes 1073741824 B"}), flush=True)
 
 
@@ -519,6 +602,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
+    ap.add_argument("--profile-mfma", action="store_true",
+                    help="counter-collection mode for the batched MFMA kernel: [gate, up] at B = 32 and 64")
     ap.add_argument("--profile", action="store_true",
                     help="counter-collection mode: only the dominant kernel (eager launches over 8 layers' "
                          "[gate, up]) and a 1 GiB elementwise copy that calibrates FETCH_SIZE / WRITE_SIZE")
@@ -539,6 +624,9 @@ def main():
     log(f"device {info}")
     if args.profile:
         profile_mode(torch, L, be)
+        return
+    if args.profile_mfma:
+        profile_mfma_mode(torch, L, be)
         return
     t0 = time.perf_counter()
     mats = build_model(torch, be)
