@@ -147,6 +147,20 @@ int jh_qmatvec_batched_dev(const jh_qmat *m, const float *d_X, int B, float *d_Y
                            int row_end, void *stream);
 int jh_qmat_dequant_dev(const jh_qmat *m, float *d_out, void *stream);
 
+/* jh_qmatvec_batched_dev without any device allocation.  No counterpart in
+ * the reference: for callers that cannot allocate (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc).  The scratch
+ * of the batched MFMA path (split-K partials, prepared x, arrival counters)
+ * is a library-static device array of 8 MiB of workspace per device instead
+ * of the stream workspace; a call that would need more fails with JH_EINVAL
+ * and says how much (jh_qmatvec_batched_dev has no such limit).  Every call
+ * on a device shares that device's array, which keeps the last call's
+ * contents: calls that overlap on one device (two streams, or a graph replay
+ * beside an eager call) race and must be ordered by the caller.  Results are
+ * those of jh_qmatvec_batched_dev, bit for bit. */
+int jh_qmatvec_batched_noalloc_dev(const jh_qmat *m, const float *d_X, int B, float *d_Y, int row_start,
+                                   int row_end, void *stream);
+
 /* n <= 8 independent GEMVs, y_i = W_i x_i over all rows of W_i, B = 1, device
  * pointers, enqueued on one stream in as few kernel launches as possible:
  * large matrices of one format that share an x (gate and up) go through one

@@ -37,6 +37,7 @@ SIGNATURES = {
     "jh_qmatvec_dev": (_I, [_P, _P, _P, _I, _I, _P]),
     "jh_qmatvec_batched_dev": (_I, [_P, _P, _I, _P, _I, _I, _P]),
     "jh_qmat_dequant_dev": (_I, [_P, _P, _P]),
+    "jh_qmatvec_batched_noalloc_dev": (_I, [_P, _P, _I, _P, _I, _I, _P]),
     "jh_qmatvec_group_dev": (_I, [_I, _P, _P, _P, _P]),
     "jh_qmatvec_batched_group_dev": (_I, [_I, _P, _P, _I, _P, _P]),
     "jh_qmatvec_swiglu_dev": (_I, [_P, _P, _P, _P, _P]),

@@ -266,7 +266,7 @@ int enqueue_mfma_group(int device, int n, const jh::MfmaDesc *d, int B, hipStrea
 // Enqueue y = W x for B vectors (device pointers), splitting B into the
 // kernel's supported batch widths, or using the MFMA path for B >= kMfmaMinBatch.
 int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int row_start, int row_end,
-                   hipStream_t s) {
+                   hipStream_t s, bool mfma = true) {
     const int nrows = row_end - row_start;
     if (nrows == 0 || B == 0) return JH_OK;
     jh::GemvArgs a;
@@ -278,7 +278,7 @@ int enqueue_matvec(const jh_qmat *m, const float *d_x, int B, float *d_y, int ro
     a.row_end = row_end;
     a.ldx = m->cols;
     a.ldy = nrows;
-    if (B >= jh::kMfmaMinBatch) {
+    if (B >= jh::kMfmaMinBatch && mfma) {
         const jh::MfmaDesc d{m->type, m->d_raw, m->pitch, m->cols, row_start, row_end, d_x, d_y};
         int rc = enqueue_mfma_group(m->ctx->device, 1, &d, B, s);
         if (rc != kMfmaNotApplicable) return rc;
@@ -586,6 +586,38 @@ int jh_qmatvec_batched_dev(const jh_qmat *m, const float *d_X, int B, float *d_Y
     if (B < 0) return fail(JH_EINVAL, "B=%d must be >= 0", B);
     if ((!d_X || !d_Y) && B > 0 && row_end > row_start) return fail(JH_EINVAL, "x and y must not be null");
     if ((rc = enqueue_matvec(m, d_X, B, d_Y, row_start, row_end, (hipStream_t)stream))) return rc;
+    return ok();
+}
+
+int jh_qmatvec_batched_noalloc_dev(const jh_qmat *m, const float *d_X, int B, float *d_Y, int row_start, int row_end,
+                                   void *stream) {
+    int rc;
+    if ((rc = check_qmat(m)) || (rc = check_range(m, row_start, row_end))) return rc;
+    if (B < 0) return fail(JH_EINVAL, "B=%d must be >= 0", B);
+    if (B == 0 || row_end == row_start) return ok();
+    if (!d_X || !d_Y) return fail(JH_EINVAL, "x and y must not be null");
+    if ((rc = set_device(m->ctx->device))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (B >= jh::kMfmaMinBatch) {
+        const jh::MfmaDesc d{m->type, m->d_raw, m->pitch, m->cols, row_start, row_end, d_X, d_Y};
+        const size_t wsb = jh::mfma_group_workspace_bytes(1, &d, B);
+        if (wsb) {
+            if (wsb > jh::kStaticScratchBytes)
+                return fail(JH_EINVAL,
+                            "rows=%d cols=%d B=%d needs %zu bytes of scratch; the static scratch holds %zu "
+                            "(jh_qmatvec_batched_dev has no such limit)",
+                            row_end - row_start, m->cols, B, wsb, jh::kStaticScratchBytes);
+            void *ws = nullptr;
+            int *counters = nullptr;
+            hipError_t e = jh::static_scratch(m->ctx->device, s, &ws, &counters);
+            if (e != hipSuccess) return hip_fail("static scratch (hipGetSymbolAddress)", e);
+            e = jh::launch_mfma_group(1, &d, B, ws, counters, s);
+            if (e == hipSuccess) return ok();
+            if (e != hipErrorNotSupported) return hip_fail("mfma_group launch", e);
+        }
+    }
+    // the kernels of the other batch sizes use no scratch
+    if ((rc = enqueue_matvec(m, d_X, B, d_Y, row_start, row_end, s, false))) return rc;
     return ok();
 }
 

@@ -85,6 +85,13 @@ hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, i
 // Which kernel launch_mfma_group takes: 0 none (the path does not apply),
 // 1 mfma_group (K split *ksplit ways), 2 x_prep + mfma_px (one unsplit matrix).
 int mfma_group_plan(int n, const MfmaDesc *d, int B, int *ksplit);
+// The file-scope device scratch of the MFMA path for callers that cannot
+// allocate (jh_qmatvec_batched_noalloc_dev): kStaticScratchBytes of workspace
+// plus the split-K counters, one copy per device.  static_scratch returns this
+// device's addresses (hipGetSymbolAddress once per device) and, on the first
+// call on a device, zeroes the counters with a kernel on stream s.
+constexpr size_t kStaticScratchBytes = 8u << 20;
+hipError_t static_scratch(int device, hipStream_t s, void **workspace, int **counters);
 // out[b][r] = silu(gate_r . x_b) * (up_r . x_b) for 3 <= B <= 32: one MFMA
 // launch whose workgroups take 128 rows of gate and the same 128 rows of up
 // (Q4_K, Q5_K, Q6_K, Q8_0; full row ranges, same shape and x).

@@ -33,6 +33,8 @@
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
 
+#include <mutex>
+
 namespace jh {
 namespace {
 
@@ -1313,6 +1315,47 @@ hipError_t launch_mfma_swiglu(const MfmaDesc &gate, const MfmaDesc &up, int B, f
         default: mfma_group<1, 8, true><<<grid, kThreads, 0, s>>>(g); break;
     }
     return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ static scratch
+// Split-K counters (kCounterSlots lines of kCounterStride ints), then
+// kStaticScratchBytes of workspace.  In host code `scratch` names a host-side
+// stand-in, not device memory: kernels get the per-device address that
+// hipGetSymbolAddress returns.  Every call on a device shares that device's
+// copy, so calls that overlap on one device race.
+constexpr size_t kStaticCounterBytes = sizeof(int) * (size_t)kCounterSlots * kCounterStride;
+static __device__ __align__(256) uint8_t scratch[kStaticCounterBytes + kStaticScratchBytes];
+
+namespace {
+__global__ void zero_words(uint32_t *p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+}  // namespace
+
+hipError_t static_scratch(int device, hipStream_t s, void **workspace, int **counters) {
+    static std::mutex mu;
+    static uint8_t *ptr[64];
+    static bool zeroed[64];
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!ptr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // the current device's copy
+        if (e != hipSuccess) return e;
+        ptr[device] = static_cast<uint8_t *>(p);
+    }
+    if (!zeroed[device]) {
+        // a kernel, not a memset: the first call may be under graph capture
+        const int n = (int)(kStaticCounterBytes / 4);
+        zero_words<<<(n + 255) / 256, 256, 0, s>>>(reinterpret_cast<uint32_t *>(ptr[device]), n);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        zeroed[device] = true;
+    }
+    *counters = reinterpret_cast<int *>(ptr[device]);
+    *workspace = ptr[device] + kStaticCounterBytes;
+    return hipSuccess;
 }
 
 hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, int *counters, hipStream_t s) {
