@@ -288,11 +288,28 @@ def step_flops(B):
     return 2 * B * (sum(r * c for _, r, c, _ in LAYER) * LAYERS + HEAD[1] * HEAD[2])
 
 
+def mfma_counters():
+    """Counter-based MFMA figures of the batched [gate, up] kernel at B = 32 / 64
+    from the committed rocprofv3 --pmc summary (profiles/)."""
+    p = os.path.join(ROOT, "profiles", "mfma_group_q4k_gate_up_b32_b64_counters.json")
+    try:
+        with open(p) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return {}
+    keep = ("kernel", "avg_us", "mfma_issued_frac_of_2p5PF", "mfma_algorithmic_frac_of_2p5PF",
+            "mfma_busy_frac_per_simd", "valu_active_frac_per_simd", "traffic_over_algorithmic")
+    return {b: dict({k: v[k] for k in keep}, source="rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_F16 / "
+                    "SQ_VALU_MFMA_BUSY_CYCLES (profiles/mfma_group_q4k_gate_up_b32_b64_counters.json)")
+            for b, v in d.get("kernels", {}).items()}
+
+
 def batch_sweep(torch, L, mats, stream, steps):
     """the 8B GEMV step at B in {8, 16, 32, 64} (grouped like
     B = 1; fp16 MFMA from B = 3).  MFMA utilisation = algorithmic flops over the
     dense fp16 peak; the kernels issue twice that (x as hi + lo fp16 limbs)."""
     out = {}
+    counters = mfma_counters()
     for B in (8, 16, 32, 64):
         launch, _ = make_step(torch, L, mats, B, stream)
         ms, _ = time_graph(torch, launch, stream, steps, 2)
@@ -301,6 +318,8 @@ def batch_sweep(torch, L, mats, stream, steps):
                         "GB_s": round(step_bytes(B) / (ms * 1e-3) / 1e9, 1), "algorithmic_TFLOP_s": round(tf, 1),
                         "mfma_util": round(tf / PEAK_MFMA_F16_TFLOPS, 4) if B >= 3 else None,
                         "mfma_issued_util": round(2 * tf / PEAK_MFMA_F16_TFLOPS, 4) if B >= 3 else None}
+        if f"b{B}" in counters:
+            out[f"b{B}"]["gate_up_kernel_counters"] = counters[f"b{B}"]
     return out
 
 
