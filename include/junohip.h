@@ -181,6 +181,25 @@ int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *
  * jh_silu_mul_dev's kernel.  Equal to that pair of calls. */
 int jh_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_x, float *d_out, void *stream);
 
+/* The FFN input norm fused into the gate / up launch: h = x + res (res may be
+ * NULL: h = x), x_out = h (when not NULL; it must not alias x or res),
+ * out[r] = silu(gate_r . xn) * (up_r . xn) with xn = rmsNorm(h, norm_w, eps).
+ * transformerLayer's x2 = x + attnProj, rmsNorm(x2) and the SwiGLU
+ * (LlamaTransformerHandler.java:778-797, rmsNorm :818-826).  Where the staged
+ * kernel applies (large matrices, cols <= 4096) one launch converts the norm's
+ * output as its input and never writes xn; otherwise jh_rmsnorm_dev into the
+ * caller's xn scratch (n floats, contents unspecified afterwards) and
+ * jh_qmatvec_swiglu_dev.  The two differ only in the summation order of
+ * mean(h^2). */
+int jh_rmsnorm_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_x, const float *d_res,
+                                  const float *d_norm_w, float eps, float *d_x_out, float *d_xn, float *d_out,
+                                  void *stream);
+
+/* The same fusion for one GEMV over all rows at B = 1: y = W rmsNorm(x + res)
+ * (the final norm and the output projection, LlamaTransformerHandler.java:803-810). */
+int jh_rmsnorm_qmatvec_dev(const jh_qmat *m, const float *d_x, const float *d_res, const float *d_norm_w, float eps,
+                           float *d_x_out, float *d_xn, float *d_y, void *stream);
+
 /* Batched form: out[b][r] = silu(gate_r . X_b) * (up_r . X_b) for B rows of X.
  * For 3 <= B <= 32 (Q4_K, Q5_K, Q6_K, Q8_0) one MFMA launch whose workgroups
  * take 128 rows of gate and the same rows of up and store the product; B = 1

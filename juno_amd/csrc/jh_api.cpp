@@ -699,6 +699,68 @@ int jh_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d
     return ok();
 }
 
+static int check_norm_args(const float *d_x, const float *d_res, const float *d_norm_w, const float *d_x_out,
+                           const float *d_xn, int n) {
+    if (!d_x || !d_norm_w || !d_xn) return fail(JH_EINVAL, "x, norm weights and xn scratch must not be null");
+    if (n < 1 || n > (1 << 20)) return fail(JH_EINVAL, "n=%d outside [1, 2^20]", n);
+    if (d_x_out && (d_x_out == d_x || d_x_out == d_res))
+        return fail(JH_EINVAL, "x_out must not alias x or res (other workgroups still read them)");
+    if (d_xn == d_x || d_xn == d_res || (d_x_out && d_xn == d_x_out)) return fail(JH_EINVAL, "xn must not alias x, res or x_out");
+    return JH_OK;
+}
+
+int jh_rmsnorm_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_x, const float *d_res,
+                                  const float *d_norm_w, float eps, float *d_x_out, float *d_xn, float *d_out,
+                                  void *stream) {
+    int rc;
+    if ((rc = check_qmat(gate)) || (rc = check_qmat(up))) return rc;
+    if (gate->rows != up->rows || gate->cols != up->cols)
+        return fail(JH_EINVAL, "gate [%d x %d] and up [%d x %d] differ in shape", gate->rows, gate->cols, up->rows,
+                    up->cols);
+    if (!d_out) return fail(JH_EINVAL, "out must not be null");
+    if ((rc = check_norm_args(d_x, d_res, d_norm_w, d_x_out, d_xn, gate->cols))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (d_res && gate->type != JH_TYPE_F32 && gemv_path() != 1) {
+        const jh::GroupProblem g{gate->type, gate->d_raw, gate->pitch, gate->cols, gate->rows, d_x, nullptr, 0, 0};
+        const jh::GroupProblem u{up->type, up->d_raw, up->pitch, up->cols, up->rows, d_x, nullptr, 0, 0};
+        const jh::NormSpec ns{d_res, d_norm_w, eps, d_x_out};
+        hipError_t e = jh::launch_gemv_swiglu(g, u, d_out, s, &ns);
+        if (e == hipSuccess) return ok();
+        if (e != hipErrorNotSupported) return hip_fail("gemv_swiglu (rmsnorm) launch", e);
+    }
+    if ((rc = jh_rmsnorm_dev(d_x, d_res, d_norm_w, gate->cols, eps, d_x_out, d_xn, stream))) return rc;
+    return jh_qmatvec_swiglu_dev(gate, up, d_xn, d_out, stream);
+}
+
+int jh_rmsnorm_qmatvec_dev(const jh_qmat *m, const float *d_x, const float *d_res, const float *d_norm_w, float eps,
+                           float *d_x_out, float *d_xn, float *d_y, void *stream) {
+    int rc;
+    if ((rc = check_qmat(m))) return rc;
+    if (!d_y) return fail(JH_EINVAL, "y must not be null");
+    if ((rc = check_norm_args(d_x, d_res, d_norm_w, d_x_out, d_xn, m->cols))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (d_res && m->type != JH_TYPE_F32 && gemv_path() != 1) {
+        jh::GemvArgs a;
+        a.type = m->type;
+        a.w = m->d_raw;
+        a.pitch = m->pitch;
+        a.cols = m->cols;
+        a.row_start = 0;
+        a.row_end = m->rows;
+        a.batch = 1;
+        a.x = d_x;
+        a.ldx = m->cols;
+        a.y = d_y;
+        a.ldy = m->rows;
+        const jh::NormSpec ns{d_res, d_norm_w, eps, d_x_out};
+        hipError_t e = jh::launch_gemv_staged(a, s, &ns);
+        if (e == hipSuccess) return ok();
+        if (e != hipErrorNotSupported) return hip_fail("gemv_staged (rmsnorm) launch", e);
+    }
+    if ((rc = jh_rmsnorm_dev(d_x, d_res, d_norm_w, m->cols, eps, d_x_out, d_xn, stream))) return rc;
+    return jh_qmatvec_dev(m, d_xn, d_y, 0, m->rows, stream);
+}
+
 int jh_qmatvec_batched_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_X, int B, float *d_out,
                                   float *d_gate, float *d_up, void *stream) {
     int rc;

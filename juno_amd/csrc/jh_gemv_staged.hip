@@ -467,6 +467,12 @@ struct StagedArgs {
     int tb;   // blocks per tile
     const float *x;
     float *swiglu;  // not null: w = {gate, up} interleaved row by row, out = silu(gate . x) * (up . x)
+    // rmsnorm prologue (NORM kernels): the GEMV input is w_n * h * scale with
+    // h = x + res and scale = 1 / sqrt(mean(h^2) + eps); workgroup 0 stores h
+    // to x_out (not aliasing x or res)
+    const float *res, *norm_w;
+    float eps;
+    float *x_out;
 };
 
 // SwiGLU pairing: virtual row v is row v / 2 of gate (v even) or up (v odd),
@@ -480,7 +486,9 @@ __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
     return p;
 }
 
-template <int T, int R, bool SX>  // SX: one column tile, x shared through an LDS image
+// SX: one column tile, x shared through an LDS image; NW: waves per workgroup;
+// NORM: x is the residual add and rmsnorm of the arguments (SX only)
+template <int T, int R, bool SX, int NW, bool NORM = false>
 __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     using F = Fmt<T>;
     constexpr int K = (F::CH + 63) / 64;  // 16-byte loads per lane per row
@@ -495,9 +503,9 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     XImage im{args.cols, nblk, lds};
     uint4 *stage = reinterpret_cast<uint4 *>(lds + (shared_x ? (XImage::bytes(nblk) + 15) & ~size_t(15) : 0));
     uint4 *buf0 = stage + wave * R * F::CH;
-    float *part = reinterpret_cast<float *>(stage + 4 * R * F::CH);  // [2][4][R]
+    float *part = reinterpret_cast<float *>(stage + NW * R * F::CH);  // [2][NW][R]
 
-    const int slots = 4 / gw;  // row groups processed side by side by one workgroup
+    const int slots = NW / gw;  // row groups processed side by side by one workgroup
     const int tile = wave % gw, slot = wave / gw;
     const int ngroups = (nrows + R - 1) / R;
     const int gstride = gridDim.x * slots;
@@ -519,11 +527,20 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     // 1. x loads, before any weight load so that waiting for x does not wait
     //    for the weight stream: with one column tile, up to 4 blocks of 256
     //    per wave for the shared image; otherwise this lane's own columns
-    constexpr int NX = SX ? 4 : (T == 8 ? 8 : 16);
+    constexpr int NXS = (16 + NW - 1) / NW;  // image blocks each wave converts (up to 16 blocks of 256)
+    constexpr int NX = SX ? NXS : (T == 8 ? 8 : 16);
     float4 xv[NX];
+    float4 rv[NORM ? NXS : 1], nwv[NORM ? NXS : 1];
     if constexpr (shared_x) {
 #pragma unroll
-        for (int k = 0; k < 4; k++) xv[k] = x_load4(args.x, args.cols, (wave + 4 * k) * 256 + lane * 4);
+        for (int k = 0; k < NXS; k++) {
+            const int c = (wave + NW * k) * 256 + lane * 4;
+            xv[k] = x_load4(args.x, args.cols, c);
+            if constexpr (NORM) {
+                rv[k] = x_load4(args.res, args.cols, c);
+                nwv[k] = x_load4(args.norm_w, args.cols, c);
+            }
+        }
     } else {
 #pragma unroll
         for (int k = 0; k < NX; k++) xv[k] = x_load4(args.x, args.cols, XRegs<T>::col(b, sub, k));
@@ -560,11 +577,38 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
 
     // 3. x into registers
     XRegs<T> xr;
+    if constexpr (NORM) {
+        // h = x + res and its sum of squares: per lane, then over the wave (DPP),
+        // then over the waves in wave order through LDS (the part area, unused
+        // until the walk); rmsNorm, LlamaTransformerHandler.java:818-826
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < NXS; k++) {
+            const int c = (wave + NW * k) * 256 + lane * 4;
+            const bool in = c < args.cols;
+            float4 h = make_float4(xv[k].x + rv[k].x, xv[k].y + rv[k].y, xv[k].z + rv[k].z, xv[k].w + rv[k].w);
+            if (!in) h = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (blockIdx.x == 0 && in && args.x_out) *reinterpret_cast<float4 *>(args.x_out + c) = h;
+            xv[k] = h;
+            ss += ((h.x * h.x + h.y * h.y) + (h.z * h.z + h.w * h.w));
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) part[wave] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) tot += part[w];
+        const float scale = 1.f / (float)sqrt((double)(tot / (float)args.cols + args.eps));
+#pragma unroll
+        for (int k = 0; k < NXS; k++)
+            xv[k] = make_float4(nwv[k].x * xv[k].x * scale, nwv[k].y * xv[k].y * scale, nwv[k].z * xv[k].z * scale,
+                                nwv[k].w * xv[k].w * scale);
+    }
     if constexpr (shared_x) {
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-            if (wave + 4 * k < nblk) x_quant_block<F::G>(im, wave + 4 * k, xv[k]);
-        for (int bx = wave + 16; bx < nblk; bx += 4)
+        for (int k = 0; k < NXS; k++)
+            if (wave + NW * k < nblk) x_quant_block<F::G>(im, wave + NW * k, xv[k]);
+        for (int bx = wave + NW * NXS; bx < nblk; bx += NW)
             x_quant_block<F::G>(im, bx, x_load4(args.x, args.cols, bx * 256 + lane * 4));
         __syncthreads();
         xr.load(im, b, sub, act);
@@ -611,7 +655,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
             }
             if (next >= ngroups) break;
         } else {
-            float *pp = part + (it & 1) * 4 * R;
+            float *pp = part + (it & 1) * NW * R;
             if (lane == 63)
 #pragma unroll
                 for (int i = 0; i < R; i++) pp[wave * R + i] = s[i];
@@ -645,27 +689,25 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     }
 }
 
-template <int T, int R, bool SX>
-__global__ __launch_bounds__(256) void gemv_staged(StagedArgs args) {
-    gemv_staged_body<T, R, SX>(args);
-}
-// the same kernel held to 168 VGPRs (three waves per SIMD)
-template <int T, int R, bool SX>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void gemv_staged_w3(StagedArgs args) {
-    gemv_staged_body<T, R, SX>(args);
+template <int T, int R, bool SX, int NW, bool NORM>
+__global__ __launch_bounds__(64 * NW) void gemv_staged(StagedArgs args) {
+    gemv_staged_body<T, R, SX, NW, NORM>(args);
 }
 
-static int staged_occupancy() {
-    static const int o = [] {
-        const char *v = getenv("JUNO_STAGED_W3");
-        return v ? atoi(v) : 0;
+// Waves per workgroup of the one-column-tile kernels: JUNO_STAGED_NW (4, 8 or
+// 12) overrides the default for tuning runs.  Column-tiled rows keep 4.
+static int staged_waves() {
+    static const int nw = [] {
+        const char *v = getenv("JUNO_STAGED_NW");
+        const int x = v ? atoi(v) : 0;
+        return (x == 4 || x == 8 || x == 12) ? x : 4;
     }();
-    return o;
+    return nw;
 }
 
 // Workgroups of `kern` with `lds` bytes of dynamic LDS that fit on the device
 // at once (at most 3 per CU).
-static int resident_workgroups(const void *kern, size_t lds) {
+static int resident_workgroups(const void *kern, int threads, size_t lds) {
     static int cus = [] {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -674,29 +716,25 @@ static int resident_workgroups(const void *kern, size_t lds) {
         return n;
     }();
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, lds) != hipSuccess || per_cu < 1) per_cu = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, lds) != hipSuccess || per_cu < 1) per_cu = 1;
     return cus * (per_cu > 3 ? 3 : per_cu);
 }
 
-template <int T, int R, bool SX>
-hipError_t launch_staged_sx(const StagedArgs &sa, size_t lds, int need, hipStream_t s) {
-    static bool attr_set = [] {
-        // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950)
-        return hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_staged<T, R, SX>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess &&
-               hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_staged_w3<T, R, SX>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
-    }();
+template <int T, int R, bool SX, int NW, bool NORM = false>
+hipError_t launch_staged_nw(const StagedArgs &sa, int nblk, int ngroups, hipStream_t s) {
+    using F = Fmt<T>;
+    const void *kern = reinterpret_cast<const void *>(&gemv_staged<T, R, SX, NW, NORM>);
+    static bool attr_set =  // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950)
+        hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
     (void)attr_set;
-    const void *kern = staged_occupancy() ? reinterpret_cast<const void *>(&gemv_staged_w3<T, R, SX>)
-                                          : reinterpret_cast<const void *>(&gemv_staged<T, R, SX>);
+    const size_t lds = (SX ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)NW * R * F::CH * 16 +
+                       2 * NW * R * 4;
+    const int slots = NW / sa.gw;
+    const int need = (ngroups + slots - 1) / slots;
     // persistent grid: as many workgroups as fit at once, capped by the work
-    int wgs = resident_workgroups(kern, lds);
+    int wgs = resident_workgroups(kern, 64 * NW, lds);
     if (wgs > need) wgs = need;
-    if (staged_occupancy())
-        gemv_staged_w3<T, R, SX><<<wgs, 256, lds, s>>>(sa);
-    else
-        gemv_staged<T, R, SX><<<wgs, 256, lds, s>>>(sa);
+    gemv_staged<T, R, SX, NW, NORM><<<wgs, 64 * NW, lds, s>>>(sa);
     return hipGetLastError();
 }
 
@@ -707,12 +745,17 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
     sa.gw = nb <= F::TBMAX ? 1 : nb <= 2 * F::TBMAX ? 2 : 4;
     sa.tb = (nb + sa.gw - 1) / sa.gw;
     const int nblk = (sa.cols + 255) / 256;
-    const size_t lds = (sa.gw == 1 ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)4 * R * F::CH * 16 +
-                       2 * 4 * R * 4;
-    const int slots = 4 / sa.gw;
     const int ngroups = (sa.nrows + R - 1) / R;
-    const int need = (ngroups + slots - 1) / slots;
-    return sa.gw == 1 ? launch_staged_sx<T, R, true>(sa, lds, need, s) : launch_staged_sx<T, R, false>(sa, lds, need, s);
+    if (sa.norm_w) {  // the rmsnorm prologue needs the shared image and every block in one pass of the waves
+        if (sa.gw != 1 || nblk > 16) return hipErrorNotSupported;
+        return launch_staged_nw<T, R, true, 4, true>(sa, nblk, ngroups, s);
+    }
+    if (sa.gw != 1) return launch_staged_nw<T, R, false, 4>(sa, nblk, ngroups, s);
+    switch (staged_waves()) {
+    case 8: return launch_staged_nw<T, R, true, 8>(sa, nblk, ngroups, s);
+    case 12: return launch_staged_nw<T, R, true, 12>(sa, nblk, ngroups, s);
+    default: return launch_staged_nw<T, R, true, 4>(sa, nblk, ngroups, s);
+    }
 }
 
 }  // namespace
@@ -765,7 +808,15 @@ constexpr size_t kStagedMinBytes = 28u << 20;
 
 static bool staged_wanted(size_t bytes) { return bytes >= kStagedMinBytes || getenv("JUNO_STAGED_R") != nullptr; }
 
-hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s) {
+static void set_norm(StagedArgs &sa, const NormSpec *norm) {
+    if (!norm) return;
+    sa.res = norm->res;
+    sa.norm_w = norm->w;
+    sa.eps = norm->eps;
+    sa.x_out = norm->x_out;
+}
+
+hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s, const NormSpec *norm) {
     if (a.batch != 1 || !staged_supported(a.type, a.cols)) return hipErrorNotSupported;
     const int nrows = a.row_end - a.row_start;
     if (!staged_wanted((size_t)nrows * a.pitch)) return hipErrorNotSupported;
@@ -781,10 +832,12 @@ hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s) {
     sa.nrows = nrows;
     sa.cols = a.cols;
     sa.x = a.x;
+    set_norm(sa, norm);
     return launch_staged_any(sa, a.type, s);
 }
 
-hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, float *out, hipStream_t s) {
+hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, float *out, hipStream_t s,
+                              const NormSpec *norm) {
     const int R = staged_rows(2);
     if (R % 2 || gate.type != up.type || gate.cols != up.cols || gate.pitch != up.pitch || gate.x != up.x ||
         gate.nrows != up.nrows || gate.nrows < 1 || !staged_supported(gate.type, gate.cols))
@@ -802,6 +855,7 @@ hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, 
     sa.cols = gate.cols;
     sa.x = gate.x;
     sa.swiglu = out;
+    set_norm(sa, norm);
     return launch_staged_any(sa, gate.type, s);
 }
 

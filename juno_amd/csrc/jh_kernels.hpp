@@ -52,12 +52,21 @@ hipError_t launch_gemv_staged_group(int n, const GroupProblem *p, hipStream_t s)
 // out[r] = silu(gate_r . x) * (up_r . x) for every row r, B = 1, one staged
 // launch that takes a row of gate and the same row of up into one row group
 // (hipErrorNotSupported where the staged kernel does not apply)
-hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, float *out, hipStream_t s);
+// The residual add and rmsnorm a staged launch can apply to its input while it
+// converts it: x_gemv = w * h * scale, h = x + res, scale = 1 / sqrt(mean(h^2)
+// + eps); workgroup 0 stores h to x_out (which aliases neither x nor res).
+struct NormSpec {
+    const float *res, *w;
+    float eps;
+    float *x_out;
+};
+hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, float *out, hipStream_t s,
+                              const NormSpec *norm = nullptr);
 
 // B = 1 coalesced, pipelined, int8-x kernel (jh_gemv_staged.hip); returns
 // hipErrorNotSupported for shapes it does not cover.
 bool staged_supported(int type, int cols);
-hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s, const NormSpec *norm = nullptr);
 
 // Batched decode through the LDS-staged, fp16-MFMA path (kMfmaMinBatch <= B <= 64).
 // Batched GEMVs (kMfmaMinBatch <= B <= 64) on fp16 MFMA: up to kMaxMfmaGroup matrices

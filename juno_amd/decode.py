@@ -256,7 +256,8 @@ class LlamaDecoder:
         f32 = dict(device=dev, dtype=torch.float32)
         self.k_cache = torch.zeros(c.num_layers, max_seq, c.kv_dim, **f32)
         self.v_cache = torch.zeros(c.num_layers, max_seq, c.kv_dim, **f32)
-        self.x = torch.zeros(c.hidden_dim, **f32)      # residual stream
+        self.x = torch.zeros(c.hidden_dim, **f32)      # residual stream (the step's input activation)
+        self.x2 = torch.zeros(c.hidden_dim, **f32)     # its ping-pong twin: a fused norm writes h = x + res here
         self.xn = torch.zeros(c.hidden_dim, **f32)     # normalised input of a projection
         self.q = torch.zeros(c.hidden_dim, **f32)
         self.k = torch.zeros(c.kv_dim, **f32)
@@ -290,11 +291,15 @@ class LlamaDecoder:
                 raise IllegalStateException("no token_embd.weight: this node takes activations")
             _check(L.jh_embed_dev(self.w.token_embd.handle, P(self.token), P(self.x), s))
         eps, nh, nkv, hd, H = c.rms_norm_eps, c.num_heads, c.num_kv_heads, c.head_dim, c.hidden_dim
+        # The residual stream alternates between x and x2: the FFN norm is fused
+        # into the gate / up launch, whose workgroups all read the residual while
+        # one of them writes the sum, so the sum goes to the other buffer.
+        cur, other = self.x, self.x2
         for li, lw in enumerate(self.w.layers):
             if li == 0:  # rmsNorm(x) (LlamaTransformerHandler.java:748)
-                _check(L.jh_rmsnorm_dev(P(self.x), None, P(lw.attn_norm), H, eps, None, P(self.xn), s))
+                _check(L.jh_rmsnorm_dev(P(cur), None, P(lw.attn_norm), H, eps, None, P(self.xn), s))
             else:        # previous layer's x2 + ffnOut (:784), then this layer's rmsNorm
-                _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(lw.attn_norm), H, eps, P(self.x), P(self.xn), s))
+                _check(L.jh_rmsnorm_dev(P(cur), P(self.proj), P(lw.attn_norm), H, eps, P(cur), P(self.xn), s))
             m = lw.mats
             self._group([m["q"], m["k"], m["v"]], [self.xn] * 3, [self.q, self.k, self.v], s)
             if lw.bias is not None:  # addInPlace of the projection biases (:758-761)
@@ -309,14 +314,16 @@ class LlamaDecoder:
             _check(L.jh_rope_attention_dev(P(self.q), P(self.k), P(self.v), nh, nkv, hd, P(self.pos), self.max_seq,
                                            c.rope_theta, P(self.k_cache[li]), P(self.v_cache[li]), P(self.att), s))
             self._group([m["o"]], [self.att], [self.proj], s)
-            # x2 = x + attnProj (:778); rmsNorm(x2) (:781)
-            _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(lw.ffn_norm), H, eps, P(self.x), P(self.xn), s))
-            # silu(gate . x2n) * (up . x2n) (:796-797): one launch pairs each gate row with its up row
-            _check(L.jh_qmatvec_swiglu_dev(m["gate"].handle, m["up"].handle, P(self.xn), P(self.hid), s))
+            # x2 = x + attnProj (:778), rmsNorm(x2) (:781) and silu(gate . x2n) * (up . x2n) (:796-797):
+            # where the staged kernel applies, one launch (the norm in its input conversion, each gate row
+            # paired with its up row); else the norm into xn and the paired GEMV
+            _check(L.jh_rmsnorm_qmatvec_swiglu_dev(m["gate"].handle, m["up"].handle, P(cur), P(self.proj),
+                                                   P(lw.ffn_norm), eps, P(other), P(self.xn), P(self.hid), s))
+            cur, other = other, cur
             self._group([m["down"]], [self.hid], [self.proj], s)
-        # final residual, rmsNorm(x, outputNorm) and the output projection (:803-810)
-        _check(L.jh_rmsnorm_dev(P(self.x), P(self.proj), P(self.w.output_norm), H, eps, P(self.x), P(self.xn), s))
-        self._group([self.w.output], [self.xn], [self.logits], s)
+        # final residual, rmsNorm(x, outputNorm) and the output projection (:803-810), fused the same way
+        _check(L.jh_rmsnorm_qmatvec_dev(self.w.output.handle, P(cur), P(self.proj), P(self.w.output_norm), eps,
+                                        P(other), P(self.xn), P(self.logits), s))
         if advance:
             _check(L.jh_pos_increment_dev(P(self.pos), 1, s))
 
