@@ -705,8 +705,31 @@ static int staged_waves() {
     return nw;
 }
 
+// Waves per workgroup of the column-tiled kernels (rows of more than 16 blocks):
+// 16 (the default), 12 or 8 share one LDS image of x between 4, 3 or 2 row groups
+// side by side, so that a CU reads x once instead of once per workgroup (per-lane
+// conversion fetched all of x per 4-wave workgroup: 44 MB from L2 for the 8B
+// ffn_down, next to its 48 MB of weights); 4 (JUNO_STAGED_WIDE=4) converts x per
+// lane into registers.
+static int staged_wide_waves() {
+    static const int nw = [] {
+        const char *v = getenv("JUNO_STAGED_WIDE");
+        const int x = v ? atoi(v) : 0;
+        return (x == 4 || x == 8 || x == 12 || x == 16) ? x : 16;
+    }();
+    return nw;
+}
+
 // Workgroups of `kern` with `lds` bytes of dynamic LDS that fit on the device
-// at once (at most 3 per CU).
+// at once (at most 3 per CU; JUNO_STAGED_PER_CU = 1..8 sets that cap for tuning runs).
+static int staged_per_cu_cap() {
+    static const int v = [] {
+        const char *e = getenv("JUNO_STAGED_PER_CU");
+        const int x = e ? atoi(e) : 0;
+        return (x >= 1 && x <= 8) ? x : 3;
+    }();
+    return v;
+}
 static int resident_workgroups(const void *kern, int threads, size_t lds) {
     static int cus = [] {
         int dev = 0, n = 0;
@@ -717,7 +740,8 @@ static int resident_workgroups(const void *kern, int threads, size_t lds) {
     }();
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, lds) != hipSuccess || per_cu < 1) per_cu = 1;
-    return cus * (per_cu > 3 ? 3 : per_cu);
+    const int cap = staged_per_cu_cap();
+    return cus * (per_cu > cap ? cap : per_cu);
 }
 
 template <int T, int R, bool SX, int NW, bool NORM = false>
@@ -729,6 +753,7 @@ hipError_t launch_staged_nw(const StagedArgs &sa, int nblk, int ngroups, hipStre
     (void)attr_set;
     const size_t lds = (SX ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)NW * R * F::CH * 16 +
                        2 * NW * R * 4;
+    if (lds > 160 * 1024) return hipErrorNotSupported;
     const int slots = NW / sa.gw;
     const int need = (ngroups + slots - 1) / slots;
     // persistent grid: as many workgroups as fit at once, capped by the work
@@ -750,7 +775,17 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
         if (sa.gw != 1 || nblk > 16) return hipErrorNotSupported;
         return launch_staged_nw<T, R, true, 4, true>(sa, nblk, ngroups, s);
     }
-    if (sa.gw != 1) return launch_staged_nw<T, R, false, 4>(sa, nblk, ngroups, s);
+    if (sa.gw != 1) {
+        hipError_t e = hipErrorNotSupported;
+        switch (staged_wide_waves()) {  // the shared image needs the LDS for it and the row groups
+        case 8: e = launch_staged_nw<T, R, true, 8>(sa, nblk, ngroups, s); break;
+        case 12: e = launch_staged_nw<T, R, true, 12>(sa, nblk, ngroups, s); break;
+        case 16: e = launch_staged_nw<T, R, true, 16>(sa, nblk, ngroups, s); break;
+        default: break;
+        }
+        if (e != hipErrorNotSupported) return e;
+        return launch_staged_nw<T, R, false, 4>(sa, nblk, ngroups, s);
+    }
     switch (staged_waves()) {
     case 8: return launch_staged_nw<T, R, true, 8>(sa, nblk, ngroups, s);
     case 12: return launch_staged_nw<T, R, true, 12>(sa, nblk, ngroups, s);
@@ -789,8 +824,20 @@ static hipError_t launch_staged_r(const StagedArgs &sa, int R, hipStream_t s) {
     }
 }
 
+// Rows per group: 2, or 1 for column-tiled rows (with the shared x image, 16 waves of
+// one row each; 8B ffn_down 20.2 -> 19.3 us, TinyLlama 10.1 -> 7.9 us, Phi-3 Q8_0
+// 13.3 -> 10.1 us).
+static bool staged_wide(int type, int nb) {
+    switch (type) {
+    case 12: return nb > Fmt<12>::TBMAX;
+    case 13: return nb > Fmt<13>::TBMAX;
+    case 14: return nb > Fmt<14>::TBMAX;
+    case 8: return nb > Fmt<8>::TBMAX;
+    default: return false;
+    }
+}
 static hipError_t launch_staged_any(const StagedArgs &sa, int type, hipStream_t s) {
-    const int R = staged_rows(2);
+    const int R = staged_rows(staged_wide(type, sa.nb) ? 1 : 2);
     switch (type) {
     case 12: return launch_staged_r<12>(sa, R, s);
     case 13: return launch_staged_r<13>(sa, R, s);
@@ -843,6 +890,9 @@ hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, 
         gate.nrows != up.nrows || gate.nrows < 1 || !staged_supported(gate.type, gate.cols))
         return hipErrorNotSupported;
     if (!staged_wanted(2 * (size_t)gate.nrows * gate.pitch)) return hipErrorNotSupported;
+    // Column-tiled rows take one row per group in the grouped launch, so that pairing
+    // cannot reproduce their sums bit for bit: the caller's grouped launch + product does.
+    if (staged_wide(gate.type, gate.type == 8 ? gate.cols / 32 : gate.cols / 256)) return hipErrorNotSupported;
     StagedArgs sa = {};
     sa.np = 2;
     sa.w[0] = gate.w;
