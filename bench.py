@@ -304,6 +304,33 @@ def mfma_counters():
             for b, v in d.get("kernels", {}).items()}
 
 
+def hbm_stream_copy(torch, stream, reps=20):
+    """STREAM-style copy on this GPU: 2 GiB of fp32 into another 2 GiB buffer
+    (torch's copy kernel), HIP events around `reps` copies; bytes = read + write.
+    The measured ceiling that HBM-bound kernels are compared with, beside the
+    8 TB/s published peak."""
+    n = 1 << 29
+    a = torch.ones(n, device="cuda")
+    b = torch.empty(n, device="cuda")
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            b.copy_(a)
+        stream.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            b.copy_(a)
+        e1.record(stream)
+        stream.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    moved = 2 * 4 * n
+    del a, b
+    torch.cuda.synchronize()
+    gbs = moved / (ms * 1e-3) / 1e9
+    return {"GB_s": round(gbs, 1), "bytes_per_copy": moved, "ms_per_copy": round(ms, 4),
+            "frac_of_peak": round(gbs / PEAK_HBM_GBS, 4)}
+
+
 def batch_sweep(torch, L, mats, stream, steps):
     """the 8B GEMV step at B in {8, 16, 32, 64} (grouped like
     B = 1; fp16 MFMA from B = 3).  MFMA utilisation = algorithmic flops over the
@@ -653,6 +680,8 @@ def main():
     log(f"model built: {len(mats)} matrices, {sum(m[4].nbytes() for m in mats) / 1e9:.3f} GB packed, "
         f"{time.perf_counter() - t0:.1f} s")
     stream = torch.cuda.Stream()
+    stream_copy = hbm_stream_copy(torch, stream)
+    log(f"HBM STREAM copy: {stream_copy}")
 
     launch, nlaunch = make_step(torch, L, mats, 1, stream)
     ms, wall_ms = time_graph(torch, launch, stream, args.steps, args.warmup)
@@ -724,6 +753,7 @@ def main():
                      "avg_launch_us": round(avg_ms * 1e3, 3),
                      "algorithmic_bytes_per_launch": per_launch},
         "cpu_baseline": cpu,
+        "hbm_stream_copy": stream_copy,
         "batched": batched,
         "batched_sweep": sweep,
         "shape_sweeps": shapes,

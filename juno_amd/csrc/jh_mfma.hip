@@ -649,6 +649,16 @@ __device__ __forceinline__ void store_tile(const f32x16 (&tot)[NT], int r, int n
                 if (b < B) __hip_atomic_store(mine + (size_t)b * nrows + r, tot[n][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
     }
+    // Ordering of the hand-off.  The partials are agent-scope atomic stores, which
+    // gfx950 performs at the memory-side coherence point (past the per-XCD L2s);
+    // s_waitcnt(0) returns only once each of this wave's stores is acknowledged
+    // there, and the barrier makes every wave's acknowledgement precede the
+    // counter's fetch_add, itself performed at that point.  The last arriver then
+    // reads the partials with agent-scope atomic loads, which are served from the
+    // same point.  A release / acquire pair on the counter would order them
+    // formally, but an agent-scope release writes back the whole L2 of the XCD
+    // (buffer_wbl2), which measured ~100 us per GEMV; there are no non-atomic
+    // stores for it to publish.
     __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have reached the coherence point
     __shared__ int s_last;
     __syncthreads();
@@ -768,7 +778,7 @@ __device__ __forceinline__ void store_pair(const f32x16 (&tot)[1], int r, int lw
                 if (b < B) __hip_atomic_store(mine + (size_t)b * 2 * nrows + vr, tot[0][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
-        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_s_waitcnt(0);  // the same hand-off ordering as store_tile
         __shared__ int s_last;
         __syncthreads();
         if (threadIdx.x == 0) {
