@@ -488,7 +488,12 @@ __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
 
 // SX: one column tile, x shared through an LDS image; NW: waves per workgroup;
 // NORM: x is the residual add and rmsnorm of the arguments (SX only)
-template <int T, int R, bool SX, int NW, bool NORM = false>
+// DYN (one column tile only): the workgroup takes a contiguous range of row
+// groups and its waves claim them one at a time from an LDS counter.  Waves
+// sharing a CU do not progress at one rate (the oldest issue first), so equal
+// static shares leave a CU with its last waves running alone; claimed groups
+// even that out.
+template <int T, int R, bool SX, int NW, bool NORM = false, bool DYN = false>
 __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     using F = Fmt<T>;
     constexpr int K = (F::CH + 63) / 64;  // 16-byte loads per lane per row
@@ -510,6 +515,15 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     const int ngroups = (nrows + R - 1) / R;
     const int gstride = gridDim.x * slots;
     int grp = blockIdx.x * slots + slot;
+    // DYN: this workgroup's groups [gbeg, gend); wave w starts with gbeg + w, then claims
+    const int gper = ngroups / (int)gridDim.x, gext = ngroups - gper * (int)gridDim.x;
+    const int gbeg = (int)blockIdx.x * gper + min((int)blockIdx.x, gext);
+    const int gend = gbeg + gper + ((int)blockIdx.x < gext ? 1 : 0);
+    int *claim = reinterpret_cast<int *>(part + 2 * NW * R);  // DYN: the next unclaimed group
+    if constexpr (DYN) {
+        grp = gbeg + wave;
+        if (threadIdx.x == 0) *claim = gbeg + NW;  // read only after the barrier of the x prologue
+    }
 
     const int blk = lane / F::LPB, sub = lane % F::LPB;
     const int b0 = tile * tb;                        // first block of this wave's tile
@@ -525,9 +539,11 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     const int lane_blk = (act ? blk : 0) * F::BB;
 
     // 1. x loads, before any weight load so that waiting for x does not wait
-    //    for the weight stream: with one column tile, up to 4 blocks of 256
-    //    per wave for the shared image; otherwise this lane's own columns
-    constexpr int NXS = (16 + NW - 1) / NW;  // image blocks each wave converts (up to 16 blocks of 256)
+    //    for the weight stream: with a shared image, every block of 256 this
+    //    wave converts (up to 16 blocks over 4 waves for one column tile, up to
+    //    64 over 8-16 waves for column tiles), all issued here rather than one
+    //    round trip per block; otherwise this lane's own columns
+    constexpr int NXS = ((NW >= 8 ? 64 : 16) + NW - 1) / NW;  // image blocks each wave converts
     constexpr int NX = SX ? NXS : (T == 8 ? 8 : 16);
     float4 xv[NX];
     float4 rv[NORM ? NXS : 1], nwv[NORM ? NXS : 1];
@@ -572,6 +588,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
             for (int k = 0; k < K; k++)
                 if (lane + 64 * k < F::CH) dst[i * F::CH + lane + 64 * k] = v[i][k];
     };
+    if constexpr (DYN) grp = grp < gend ? grp : ngroups;  // a range shorter than the waves: nothing to do
     issue(grp);
     asm volatile("" ::: "memory");
 
@@ -626,7 +643,13 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
         int cstart[R];
 #pragma unroll
         for (int i = 0; i < R; i++) cstart[i] = start[i];
-        const int next = grp + gstride;
+        int next = grp + gstride;
+        if constexpr (DYN) {
+            int c = 0;
+            if (lane == 0) c = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            next = __builtin_amdgcn_readfirstlane(c);
+            next = next < gend ? next : ngroups;  // past the range: the loads below repeat the last group
+        }
         issue(next);
         const int r0 = grp * R;
         const uint8_t *cb = reinterpret_cast<const uint8_t *>(buf0);
@@ -689,13 +712,27 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     }
 }
 
-template <int T, int R, bool SX, int NW, bool NORM>
+template <int T, int R, bool SX, int NW, bool NORM, bool DYN>
 __global__ __launch_bounds__(64 * NW) void gemv_staged(StagedArgs args) {
-    gemv_staged_body<T, R, SX, NW, NORM>(args);
+    gemv_staged_body<T, R, SX, NW, NORM, DYN>(args);
 }
 
-// Waves per workgroup of the one-column-tile kernels: JUNO_STAGED_NW (4, 8 or
-// 12) overrides the default for tuning runs.  Column-tiled rows keep 4.
+// One-column-tile rows take one 12-wave workgroup per CU whose waves claim row
+// groups (DYN), unless JUNO_STAGED_DYN=0: then 4-wave workgroups, up to 3 per CU,
+// with equal static shares (JUNO_STAGED_NW = 8 or 12 widens them), for A/B runs.
+// Measured with per-workgroup timestamps on the static layout: on the 8B lm_head
+// the first workgroup on each CU ended at ~53 us, the second at ~62, the third at
+// ~73 us (the CU issues its oldest waves first).
+static bool staged_dyn() {
+    static const bool on = [] {
+        const char *v = getenv("JUNO_STAGED_DYN");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
+// Waves per workgroup of the static one-column-tile kernels: JUNO_STAGED_NW (4,
+// 8 or 12) overrides the default for tuning runs.
 static int staged_waves() {
     static const int nw = [] {
         const char *v = getenv("JUNO_STAGED_NW");
@@ -730,7 +767,7 @@ static int staged_per_cu_cap() {
     }();
     return v;
 }
-static int resident_workgroups(const void *kern, int threads, size_t lds) {
+static int cu_count() {
     static int cus = [] {
         int dev = 0, n = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -738,28 +775,32 @@ static int resident_workgroups(const void *kern, int threads, size_t lds) {
             n = 256;
         return n;
     }();
+    return cus;
+}
+static int resident_workgroups(const void *kern, int threads, size_t lds) {
+    const int cus = cu_count();
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, lds) != hipSuccess || per_cu < 1) per_cu = 1;
     const int cap = staged_per_cu_cap();
     return cus * (per_cu > cap ? cap : per_cu);
 }
 
-template <int T, int R, bool SX, int NW, bool NORM = false>
+template <int T, int R, bool SX, int NW, bool NORM = false, bool DYN = false>
 hipError_t launch_staged_nw(const StagedArgs &sa, int nblk, int ngroups, hipStream_t s) {
     using F = Fmt<T>;
-    const void *kern = reinterpret_cast<const void *>(&gemv_staged<T, R, SX, NW, NORM>);
+    const void *kern = reinterpret_cast<const void *>(&gemv_staged<T, R, SX, NW, NORM, DYN>);
     static bool attr_set =  // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950)
         hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
     (void)attr_set;
     const size_t lds = (SX ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)NW * R * F::CH * 16 +
-                       2 * NW * R * 4;
+                       2 * NW * R * 4 + 16;
     if (lds > 160 * 1024) return hipErrorNotSupported;
     const int slots = NW / sa.gw;
     const int need = (ngroups + slots - 1) / slots;
-    // persistent grid: as many workgroups as fit at once, capped by the work
-    int wgs = resident_workgroups(kern, 64 * NW, lds);
+    // persistent grid: as many workgroups as fit at once (DYN: one per CU), capped by the work
+    int wgs = DYN ? cu_count() : resident_workgroups(kern, 64 * NW, lds);
     if (wgs > need) wgs = need;
-    gemv_staged<T, R, SX, NW, NORM><<<wgs, 64 * NW, lds, s>>>(sa);
+    gemv_staged<T, R, SX, NW, NORM, DYN><<<wgs, 64 * NW, lds, s>>>(sa);
     return hipGetLastError();
 }
 
@@ -773,6 +814,7 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
     const int ngroups = (sa.nrows + R - 1) / R;
     if (sa.norm_w) {  // the rmsnorm prologue needs the shared image and every block in one pass of the waves
         if (sa.gw != 1 || nblk > 16) return hipErrorNotSupported;
+        if (staged_dyn()) return launch_staged_nw<T, R, true, 12, true, true>(sa, nblk, ngroups, s);
         return launch_staged_nw<T, R, true, 4, true>(sa, nblk, ngroups, s);
     }
     if (sa.gw != 1) {
@@ -786,6 +828,7 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
         if (e != hipErrorNotSupported) return e;
         return launch_staged_nw<T, R, false, 4>(sa, nblk, ngroups, s);
     }
+    if (staged_dyn()) return launch_staged_nw<T, R, true, 12, false, true>(sa, nblk, ngroups, s);
     switch (staged_waves()) {
     case 8: return launch_staged_nw<T, R, true, 8>(sa, nblk, ngroups, s);
     case 12: return launch_staged_nw<T, R, true, 12>(sa, nblk, ngroups, s);

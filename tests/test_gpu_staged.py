@@ -1,9 +1,10 @@
 """Parity of the staged B=1 kernel on every shape it supports.
 
 By default the library uses the staged kernel only for matrices of >= 28 MB
-(it wins there); JUNO_STAGED_R forces it for all sizes.  The check runs in one
-child process with that variable set, against the CPU oracle, to the bar of
-the parity suite: max rel-err 1e-3 with eps_r = 1e-3 * sum_c |w_rc x_c|.
+(it wins there); JUNO_STAGED_R forces it for all sizes (and sets the rows per
+group).  Each check runs in one child process with the variables set, against
+the CPU oracle, to the bar of the parity suite: max rel-err 1e-3 with
+eps_r = 1e-3 * sum_c |w_rc x_c|.
 """
 import os
 import subprocess
@@ -78,8 +79,15 @@ print("staged-ok", worst)
 '''
 
 
-def test_staged_kernel_all_shapes():
-    env = dict(os.environ, JUNO_STAGED_R="2")
+@pytest.mark.parametrize("rows_per_group,wide", [("2", None), ("1", None), ("2", "4")],
+                         ids=["two rows", "one row (wide default)", "per-lane x for column tiles"])
+def test_staged_kernel_all_shapes(rows_per_group, wide):
+    """Every shape through the staged kernel with two rows per group, with one
+    (the default for column-tiled rows: 16 waves sharing one LDS image of x), and
+    with column-tiled rows converting x per lane (JUNO_STAGED_WIDE=4)."""
+    env = dict(os.environ, JUNO_STAGED_R=rows_per_group)
+    if wide:
+        env["JUNO_STAGED_WIDE"] = wide
     r = subprocess.run([sys.executable, "-u", "-c", CHILD], env=env, cwd=ROOT, capture_output=True,
                        text=True, timeout=300)
     print(r.stdout[-3000:])
