@@ -200,6 +200,20 @@ int jh_rmsnorm_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const 
 int jh_rmsnorm_qmatvec_dev(const jh_qmat *m, const float *d_x, const float *d_res, const float *d_norm_w, float eps,
                            float *d_x_out, float *d_xn, float *d_y, void *stream);
 
+/* The attention input norm fused into the grouped GEMV of the matrices that
+ * read it: h = x + res, x_out = h (when not NULL; it must not alias x or res),
+ * y_i = W_i rmsNorm(h, norm_w, eps) for n <= 8 matrices of one column count
+ * (q, k, v: transformerLayer's rmsNorm and three matVecs,
+ * LlamaTransformerHandler.java:749-757, rmsNorm :818-826).  With res given and
+ * quantized matrices one one-shot launch forms w_n * h in each workgroup's LDS,
+ * applies the norm's scale to its sums and never writes xn (cols <= 8192);
+ * otherwise jh_rmsnorm_dev into the caller's xn scratch (cols floats) and
+ * jh_qmatvec_group_dev.  The two differ only in where the scale is applied
+ * and the summation order of mean(h^2). */
+int jh_rmsnorm_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *d_x, const float *d_res,
+                                 const float *d_norm_w, float eps, float *d_x_out, float *d_xn, float *const *d_y,
+                                 void *stream);
+
 /* Batched form: out[b][r] = silu(gate_r . X_b) * (up_r . X_b) for B rows of X.
  * For 3 <= B <= 32 (Q4_K, Q5_K, Q6_K, Q8_0) one MFMA launch whose workgroups
  * take 128 rows of gate and the same rows of up and store the product; B = 1

@@ -43,6 +43,7 @@ SIGNATURES = {
     "jh_qmatvec_swiglu_dev": (_I, [_P, _P, _P, _P, _P]),
     "jh_rmsnorm_qmatvec_swiglu_dev": (_I, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _P]),
     "jh_rmsnorm_qmatvec_dev": (_I, [_P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _P]),
+    "jh_rmsnorm_qmatvec_group_dev": (_I, [_I, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _P]),
     "jh_qmatvec_batched_swiglu_dev": (_I, [_P, _P, _P, _I, _P, _P, _P, _P]),
     "jh_qmatvec_batched_plan": (_I, [_I, _P, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "jh_stream_workspace_info": (_I, [_I, _P, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(_P)]),

@@ -761,6 +761,44 @@ int jh_rmsnorm_qmatvec_dev(const jh_qmat *m, const float *d_x, const float *d_re
     return jh_qmatvec_dev(m, d_xn, d_y, 0, m->rows, stream);
 }
 
+int jh_rmsnorm_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *d_x, const float *d_res,
+                                 const float *d_norm_w, float eps, float *d_x_out, float *d_xn, float *const *d_y,
+                                 void *stream) {
+    if (n < 1 || n > jh::kMaxGroup) return fail(JH_EINVAL, "n=%d outside [1, %d]", n, jh::kMaxGroup);
+    if (!mats || !d_y) return fail(JH_EINVAL, "mats and y must not be null");
+    int rc;
+    for (int i = 0; i < n; i++) {
+        if ((rc = check_qmat(mats[i]))) return rc;
+        if (!d_y[i]) return fail(JH_EINVAL, "y[%d] must not be null", i);
+        if (mats[i]->cols != mats[0]->cols)
+            return fail(JH_EINVAL, "matrix %d has %d columns, matrix 0 has %d (one input for all)", i, mats[i]->cols,
+                        mats[0]->cols);
+        if (mats[i]->ctx->device != mats[0]->ctx->device) return fail(JH_EINVAL, "matrices on different devices");
+    }
+    const int cols = mats[0]->cols;
+    if ((rc = check_norm_args(d_x, d_res, d_norm_w, d_x_out, d_xn, cols))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    bool fused = d_res && gemv_path() != 1;
+    for (int i = 0; i < n; i++) fused = fused && mats[i]->type != JH_TYPE_F32;
+    if (fused) {
+        jh::GroupArgs g = {};
+        for (int i = 0; i < n; i++)
+            g.p[g.n++] = jh::GroupProblem{mats[i]->type, mats[i]->d_raw, mats[i]->pitch, cols, mats[i]->rows, d_x,
+                                          d_y[i], 0, 0};
+        g.res = d_res;
+        g.norm_w = d_norm_w;
+        g.eps = eps;
+        g.x_out = d_x_out;
+        hipError_t e = jh::launch_gemv_group(g, s);
+        if (e == hipSuccess) return ok();
+        if (e != hipErrorNotSupported) return hip_fail("gemv_group (rmsnorm) launch", e);
+    }
+    if ((rc = jh_rmsnorm_dev(d_x, d_res, d_norm_w, cols, eps, d_x_out, d_xn, stream))) return rc;
+    const float *xs[jh::kMaxGroup];
+    for (int i = 0; i < n; i++) xs[i] = d_xn;
+    return jh_qmatvec_group_dev(n, mats, xs, d_y, stream);
+}
+
 int jh_qmatvec_batched_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d_X, int B, float *d_out,
                                   float *d_gate, float *d_up, void *stream) {
     int rc;

@@ -29,7 +29,7 @@ namespace jh {
 template <int R, int B, bool Q5 = false>
 __device__ __forceinline__ void gemv_q4k_body(int wg, const uint8_t *__restrict__ W, size_t pitch, int nb,
                                                 int nrows, const float *__restrict__ X, int ldx,
-                                                float *__restrict__ Y, int ldy) {
+                                                float *__restrict__ Y, int ldy, float ysc = 1.f) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r0 = (wg * 4 + wave) * R;
     if (r0 >= nrows) return;
@@ -112,7 +112,7 @@ __device__ __forceinline__ void gemv_q4k_body(int wg, const uint8_t *__restrict_
 #pragma unroll
         for (int j = 0; j < B; j++) {
             float s = wave_sum(acc[i][j]);
-            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s * ysc;
         }
 }
 
@@ -123,7 +123,7 @@ __device__ __forceinline__ void gemv_q4k_body(int wg, const uint8_t *__restrict_
 template <int R, int B>
 __device__ __forceinline__ void gemv_q6k_body(int wg, const uint8_t *__restrict__ W, size_t pitch, int nb,
                                                 int nrows, const float *__restrict__ X, int ldx,
-                                                float *__restrict__ Y, int ldy) {
+                                                float *__restrict__ Y, int ldy, float ysc = 1.f) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r0 = (wg * 4 + wave) * R;
     if (r0 >= nrows) return;
@@ -212,7 +212,7 @@ __device__ __forceinline__ void gemv_q6k_body(int wg, const uint8_t *__restrict_
 #pragma unroll
         for (int j = 0; j < B; j++) {
             float s = wave_sum(acc[i][j]);
-            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s * ysc;
         }
 }
 
@@ -226,7 +226,7 @@ __device__ __forceinline__ void gemv_q6k_body(int wg, const uint8_t *__restrict_
 template <int R, int B>
 __device__ __forceinline__ void gemv_q2k_body(int wg, const uint8_t *__restrict__ W, size_t pitch, int nb,
                                                 int nrows, const float *__restrict__ X, int ldx,
-                                                float *__restrict__ Y, int ldy) {
+                                                float *__restrict__ Y, int ldy, float ysc = 1.f) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r0 = (wg * 4 + wave) * R;
     if (r0 >= nrows) return;
@@ -302,7 +302,7 @@ __device__ __forceinline__ void gemv_q2k_body(int wg, const uint8_t *__restrict_
 #pragma unroll
         for (int j = 0; j < B; j++) {
             float s = wave_sum(acc[i][j]);
-            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s * ysc;
         }
 }
 
@@ -316,7 +316,7 @@ __device__ __forceinline__ void gemv_q2k_body(int wg, const uint8_t *__restrict_
 template <int R, int B>
 __device__ __forceinline__ void gemv_q3k_body(int wg, const uint8_t *__restrict__ W, size_t pitch, int nb,
                                                 int nrows, const float *__restrict__ X, int ldx,
-                                                float *__restrict__ Y, int ldy) {
+                                                float *__restrict__ Y, int ldy, float ysc = 1.f) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r0 = (wg * 4 + wave) * R;
     if (r0 >= nrows) return;
@@ -394,7 +394,7 @@ __device__ __forceinline__ void gemv_q3k_body(int wg, const uint8_t *__restrict_
 #pragma unroll
         for (int j = 0; j < B; j++) {
             float s = wave_sum(acc[i][j]);
-            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s * ysc;
         }
 }
 
@@ -404,7 +404,7 @@ __device__ __forceinline__ void gemv_q3k_body(int wg, const uint8_t *__restrict_
 template <int R, int B>
 __device__ __forceinline__ void gemv_q8_0_body(int wg, const uint8_t *__restrict__ W, size_t pitch, int nb,
                                                  int nrows, const float *__restrict__ X, int ldx,
-                                                 float *__restrict__ Y, int ldy) {
+                                                 float *__restrict__ Y, int ldy, float ysc = 1.f) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r0 = (wg * 4 + wave) * R;
     if (r0 >= nrows) return;
@@ -469,7 +469,7 @@ __device__ __forceinline__ void gemv_q8_0_body(int wg, const uint8_t *__restrict
 #pragma unroll
         for (int j = 0; j < B; j++) {
             float s = wave_sum(acc[i][j]);
-            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s;
+            if (lane == 0 && r0 + i < nrows) Y[(size_t)j * ldy + r0 + i] = s * ysc;
         }
 }
 
@@ -509,6 +509,14 @@ __global__ __launch_bounds__(256) void gemv_q8_0(const uint8_t *__restrict__ W, 
 // workgroups [wg_begin[p], wg_begin[p+1]) belong to problem p.  One launch
 // instead of n removes the per-launch ramp and drain that dominate small
 // matrices (a Llama-3-8B k projection streams 2.4 MB, ~0.4 us at HBM speed).
+//
+// NORM: every problem's x is w_n * h * scale with h = x + res (the first
+// problem's x) and scale = 1 / sqrt(mean(h^2) + eps) (rmsNorm,
+// LlamaTransformerHandler.java:818-826).  Each workgroup forms w_n * h for all
+// columns in LDS and sums h^2 in the same pass; the bodies read x from there and
+// multiply their sums by the scale, so the norm costs one pass over three
+// vectors instead of a launch.  Workgroup 0 stores h to x_out.
+template <bool NORM>
 __global__ __launch_bounds__(256) void gemv_group(GroupArgs g) {
     const int bid = blockIdx.x;
     int p = 0;
@@ -518,23 +526,56 @@ __global__ __launch_bounds__(256) void gemv_group(GroupArgs g) {
     const GroupProblem &q = g.p[p];
     const int wg = bid - q.wg_begin;
     const int nb = q.type == 8 ? q.cols / 32 : q.cols / 256;
+    const float *X = q.x;
+    float ysc = 1.f;
+    if constexpr (NORM) {
+        extern __shared__ __align__(16) float xs[];
+        __shared__ float part[4];
+        const int cols = q.cols;
+        float4 hv[kNormGroupMaxCols / 1024], wv[kNormGroupMaxCols / 1024];
+        // every load first (addresses clamped in range), then the arithmetic
+#pragma unroll
+        for (int k = 0; k < kNormGroupMaxCols / 1024; k++) {
+            const int c = min((int)threadIdx.x * 4 + 1024 * k, cols - 4);
+            const float4 a = load_f4(X + c), r = load_f4(g.res + c);
+            hv[k] = make_float4(a.x + r.x, a.y + r.y, a.z + r.z, a.w + r.w);
+            wv[k] = load_f4(g.norm_w + c);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < kNormGroupMaxCols / 1024; k++) {
+            const int c = (int)threadIdx.x * 4 + 1024 * k;
+            if (c < cols) {
+                const float4 h = hv[k], w = wv[k];
+                if (bid == 0 && g.x_out) *reinterpret_cast<float4 *>(g.x_out + c) = h;
+                *reinterpret_cast<float4 *>(xs + c) = make_float4(w.x * h.x, w.y * h.y, w.z * h.z, w.w * h.w);
+                ss += (h.x * h.x + h.y * h.y) + (h.z * h.z + h.w * h.w);
+            }
+        }
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+        ysc = 1.f / (float)sqrt((double)(tot / (float)cols + g.eps));
+        X = xs;
+    }
     if (q.rows_per_wave == 2) {
         switch (q.type) {
-        case 12: gemv_q4k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        case 13: gemv_q4k_body<2, 1, true>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        case 14: gemv_q6k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        case 10: gemv_q2k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        case 11: gemv_q3k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        default: gemv_q8_0_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
+        case 12: gemv_q4k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        case 13: gemv_q4k_body<2, 1, true>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        case 14: gemv_q6k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        case 10: gemv_q2k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        case 11: gemv_q3k_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        default: gemv_q8_0_body<2, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
         }
     } else {
         switch (q.type) {
-        case 12: gemv_q4k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        case 13: gemv_q4k_body<1, 1, true>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        case 14: gemv_q6k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        case 10: gemv_q2k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        case 11: gemv_q3k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
-        default: gemv_q8_0_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, q.x, q.cols, q.y, q.nrows); break;
+        case 12: gemv_q4k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        case 13: gemv_q4k_body<1, 1, true>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        case 14: gemv_q6k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        case 10: gemv_q2k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        case 11: gemv_q3k_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
+        default: gemv_q8_0_body<1, 1>(wg, q.w, q.pitch, nb, q.nrows, X, q.cols, q.y, q.nrows, ysc); break;
         }
     }
 }
@@ -550,7 +591,16 @@ hipError_t launch_gemv_group(GroupArgs g, hipStream_t s) {
         total += (q.nrows + 4 * q.rows_per_wave - 1) / (4 * q.rows_per_wave);
     }
     if (total == 0) return hipSuccess;
-    gemv_group<<<total, 256, 0, s>>>(g);
+    if (g.norm_w) {
+        // one input for all problems, its columns a multiple of 4 and within the LDS image
+        for (int i = 0; i < g.n; i++)
+            if (g.p[i].x != g.p[0].x || g.p[i].cols != g.p[0].cols) return hipErrorNotSupported;
+        const int cols = g.p[0].cols;
+        if (!g.res || cols % 4 || cols > kNormGroupMaxCols) return hipErrorNotSupported;
+        gemv_group<true><<<total, 256, (size_t)cols * sizeof(float), s>>>(g);
+    } else {
+        gemv_group<false><<<total, 256, 0, s>>>(g);
+    }
     return hipGetLastError();
 }
 

@@ -478,6 +478,9 @@ struct StagedArgs {
 // SwiGLU pairing: virtual row v is row v / 2 of gate (v even) or up (v odd),
 // so that a row group (R even) holds both halves of its outputs.
 
+// cells per slot of the column-tile ring (a power of two)
+constexpr int kRing = 4;
+
 __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
     int p = 0;
 #pragma unroll
@@ -508,7 +511,11 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     XImage im{args.cols, nblk, lds};
     uint4 *stage = reinterpret_cast<uint4 *>(lds + (shared_x ? (XImage::bytes(nblk) + 15) & ~size_t(15) : 0));
     uint4 *buf0 = stage + wave * R * F::CH;
-    float *part = reinterpret_cast<float *>(stage + NW * R * F::CH);  // [2][NW][R]
+    // partial sums of column-tiled rows: [kRing][NW][R] (the shared-x ring below)
+    // or [2][NW][R] (per-lane x), then the ring's arrival and release counters
+    float *part = reinterpret_cast<float *>(stage + NW * R * F::CH);
+    int *ring_arr = reinterpret_cast<int *>(part + kRing * NW * R);  // [slot][cell]: arrivals
+    int *ring_done = ring_arr + kRing * NW;                            // [slot][cell]: uses finished
 
     const int slots = NW / gw;  // row groups processed side by side by one workgroup
     const int tile = wave % gw, slot = wave / gw;
@@ -519,7 +526,9 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     const int gper = ngroups / (int)gridDim.x, gext = ngroups - gper * (int)gridDim.x;
     const int gbeg = (int)blockIdx.x * gper + min((int)blockIdx.x, gext);
     const int gend = gbeg + gper + ((int)blockIdx.x < gext ? 1 : 0);
-    int *claim = reinterpret_cast<int *>(part + 2 * NW * R);  // DYN: the next unclaimed group
+    int *claim = ring_done + kRing * NW;  // DYN: the next unclaimed group
+    // the ring's counters start at zero; read only after the barrier of the x prologue
+    if (SX && (int)threadIdx.x < 2 * kRing * NW) ring_arr[threadIdx.x] = 0;
     if constexpr (DYN) {
         grp = gbeg + wave;
         if (threadIdx.x == 0) *claim = gbeg + NW;  // read only after the barrier of the x prologue
@@ -636,6 +645,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     }
 
     // 4. pipelined walk over row groups
+    if (SX && gw != 1 && grp >= ngroups) return;  // fewer groups than slots: this slot has none
     park(buf0);
     wave_lds_sync();
     int it = 0;
@@ -674,6 +684,51 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
 #pragma unroll
                     for (int i = 0; i < R; i++)
                         if (r0 + i < nrows) store(r0 + i, s[i]);
+                }
+            }
+            if (next >= ngroups) break;
+        } else if constexpr (SX) {
+            // Column tiles meet in a ring of kRing cells per slot instead of at a
+            // workgroup barrier, so that a wave's arithmetic overlaps the other
+            // waves' loads.  The gw waves of a slot walk the same groups in the same
+            // order; the it-th group uses cell it % kRing for the (it / kRing)-th
+            // time.  A wave first waits until that cell's previous use is finished
+            // (the slowest wave never waits, so the waits end), writes its partial
+            // sums, and counts its arrival; the last of the gw waves adds the
+            // partials in tile order (as the barrier version did) and stores y.
+            const int cell = slot * kRing + (it & (kRing - 1));
+            const int use = it / kRing;
+            if (use > 0)
+                for (int spin = 0; spin < (1 << 22); spin++) {
+                    if (__hip_atomic_load(ring_done + cell, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= use) break;
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            float *pc = part + cell * gw * R;
+            int a = 0;
+            if (lane == 63) {
+#pragma unroll
+                for (int i = 0; i < R; i++) pc[tile * R + i] = s[i];
+                a = __hip_atomic_fetch_add(ring_arr + cell, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            a = __builtin_amdgcn_readlane(a, 63);
+            if (a == use * gw + gw - 1) {  // the last arrival for this group
+                if (lane == 63) {
+                    float t[R];
+#pragma unroll
+                    for (int i = 0; i < R; i++) {
+                        t[i] = 0.f;
+                        for (int q = 0; q < gw; q++) t[i] += pc[q * R + i];
+                    }
+                    if (args.swiglu) {
+#pragma unroll
+                        for (int i = 0; i + 1 < R; i += 2)
+                            if (r0 + i < nrows) args.swiglu[(r0 + i) >> 1] = silu_times(t[i], t[i + 1]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < R; i++)
+                            if (r0 + i < nrows) store(r0 + i, t[i]);
+                    }
+                    __hip_atomic_store(ring_done + cell, use + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
             }
             if (next >= ngroups) break;
@@ -793,7 +848,7 @@ hipError_t launch_staged_nw(const StagedArgs &sa, int nblk, int ngroups, hipStre
         hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
     (void)attr_set;
     const size_t lds = (SX ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)NW * R * F::CH * 16 +
-                       2 * NW * R * 4 + 16;
+                       kRing * NW * R * 4 + 2 * kRing * NW * 4 + 16;
     if (lds > 160 * 1024) return hipErrorNotSupported;
     const int slots = NW / sa.gw;
     const int need = (ngroups + slots - 1) / slots;
@@ -894,9 +949,32 @@ static hipError_t launch_staged_any(const StagedArgs &sa, int type, hipStream_t 
 // few microseconds; below ~28 MB of packed weights per launch the one-shot
 // kernels of jh_gemv.hip finish first (measured on MI355X at Llama-3-8B and
 // Phi-3 shapes).  JUNO_STAGED_R set forces the staged kernel (tests, tuning).
+// Column-tiled rows (16 waves sharing x, no barrier between row groups) win
+// from ~16 MB over rotated copies (Phi-3 Q6_K ffn_down 20.6 MB: 16.0 -> 11.3 us,
+// Q8_0 26.7 MB: 12.6 -> 9.8 us), but not at the TinyLlama ffn_down (9.5 MB),
+// whose input arrives from the previous launch (+0.8 us per layer in the step).
+// A launch that also carries the residual add + rmsnorm saves a launch of its
+// own, which pays for the prologue from ~8 MB (TinyLlama [gate, up], 13 MB).
 constexpr size_t kStagedMinBytes = 28u << 20;
+constexpr size_t kStagedMinWideBytes = 16u << 20;
+constexpr size_t kStagedMinFusedBytes = 8u << 20;
 
-static bool staged_wanted(size_t bytes) { return bytes >= kStagedMinBytes || getenv("JUNO_STAGED_R") != nullptr; }
+// Thresholds in MB: JUNO_STAGED_MIN (one column tile), JUNO_STAGED_MIN_WIDE
+// (column-tiled rows) and JUNO_STAGED_MIN_FUSED (with the rmsnorm prologue)
+// override the defaults for tuning runs.
+static size_t env_mb(const char *name, size_t def) {
+    const char *v = getenv(name);
+    return v ? (size_t)atoi(v) << 20 : def;
+}
+static bool staged_wanted(size_t bytes, int type, int cols, bool fused = false) {
+    static const size_t narrow = env_mb("JUNO_STAGED_MIN", kStagedMinBytes);
+    static const size_t wideb = env_mb("JUNO_STAGED_MIN_WIDE", kStagedMinWideBytes);
+    static const size_t fusedb = env_mb("JUNO_STAGED_MIN_FUSED", kStagedMinFusedBytes);
+    const bool wide = staged_wide(type, type == 8 ? cols / 32 : cols / 256);
+    size_t min = wide ? wideb : narrow;
+    if (fused && fusedb < min) min = fusedb;
+    return bytes >= min || getenv("JUNO_STAGED_R") != nullptr;
+}
 
 static void set_norm(StagedArgs &sa, const NormSpec *norm) {
     if (!norm) return;
@@ -909,7 +987,7 @@ static void set_norm(StagedArgs &sa, const NormSpec *norm) {
 hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s, const NormSpec *norm) {
     if (a.batch != 1 || !staged_supported(a.type, a.cols)) return hipErrorNotSupported;
     const int nrows = a.row_end - a.row_start;
-    if (!staged_wanted((size_t)nrows * a.pitch)) return hipErrorNotSupported;
+    if (!staged_wanted((size_t)nrows * a.pitch, a.type, a.cols, norm != nullptr)) return hipErrorNotSupported;
     StagedArgs sa = {};
     sa.np = 1;
     sa.w[0] = a.w;
@@ -932,7 +1010,7 @@ hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, 
     if (R % 2 || gate.type != up.type || gate.cols != up.cols || gate.pitch != up.pitch || gate.x != up.x ||
         gate.nrows != up.nrows || gate.nrows < 1 || !staged_supported(gate.type, gate.cols))
         return hipErrorNotSupported;
-    if (!staged_wanted(2 * (size_t)gate.nrows * gate.pitch)) return hipErrorNotSupported;
+    if (!staged_wanted(2 * (size_t)gate.nrows * gate.pitch, gate.type, gate.cols, norm != nullptr)) return hipErrorNotSupported;
     // Column-tiled rows take one row per group in the grouped launch, so that pairing
     // cannot reproduce their sums bit for bit: the caller's grouped launch + product does.
     if (staged_wide(gate.type, gate.type == 8 ? gate.cols / 32 : gate.cols / 256)) return hipErrorNotSupported;
@@ -961,7 +1039,7 @@ hipError_t launch_gemv_staged_group(int n, const GroupProblem *p, hipStream_t s)
             return hipErrorNotSupported;
         bytes += (size_t)p[i].nrows * p[i].pitch;
     }
-    if (!staged_wanted(bytes)) return hipErrorNotSupported;
+    if (!staged_wanted(bytes, p[0].type, p[0].cols)) return hipErrorNotSupported;
     StagedArgs sa = {};
     sa.np = n;
     int total = 0;

@@ -41,7 +41,13 @@ struct GroupProblem {
 struct GroupArgs {
     int n;
     GroupProblem p[kMaxGroup];
+    // optional residual add + rmsnorm of the (shared) input: x = w_n * (x + res) * scale,
+    // h = x + res stored to x_out; hipErrorNotSupported where it does not apply
+    const float *res = nullptr, *norm_w = nullptr;
+    float eps = 0.f;
+    float *x_out = nullptr;
 };
+constexpr int kNormGroupMaxCols = 8192;  // the LDS image of the normalised input
 hipError_t launch_gemv_group(GroupArgs g, hipStream_t s);
 
 // Large same-format matrices sharing one x (e.g. gate and up) through the

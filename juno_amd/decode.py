@@ -291,17 +291,28 @@ class LlamaDecoder:
                 raise IllegalStateException("no token_embd.weight: this node takes activations")
             _check(L.jh_embed_dev(self.w.token_embd.handle, P(self.token), P(self.x), s))
         eps, nh, nkv, hd, H = c.rms_norm_eps, c.num_heads, c.num_kv_heads, c.head_dim, c.hidden_dim
-        # The residual stream alternates between x and x2: the FFN norm is fused
-        # into the gate / up launch, whose workgroups all read the residual while
-        # one of them writes the sum, so the sum goes to the other buffer.
+        # The residual stream alternates between x and x2: the norms are fused
+        # into the q / k / v and gate / up launches, whose workgroups all read the
+        # residual while one of them writes the sum, so the sum goes to the other
+        # buffer.
         cur, other = self.x, self.x2
         for li, lw in enumerate(self.w.layers):
+            m = lw.mats
             if li == 0:  # rmsNorm(x) (LlamaTransformerHandler.java:748)
                 _check(L.jh_rmsnorm_dev(P(cur), None, P(lw.attn_norm), H, eps, None, P(self.xn), s))
-            else:        # previous layer's x2 + ffnOut (:784), then this layer's rmsNorm
+                self._group([m["q"], m["k"], m["v"]], [self.xn] * 3, [self.q, self.k, self.v], s)
+            elif self.lora is not None:  # the adapters read the normalised input: keep it in xn
                 _check(L.jh_rmsnorm_dev(P(cur), P(self.proj), P(lw.attn_norm), H, eps, P(cur), P(self.xn), s))
-            m = lw.mats
-            self._group([m["q"], m["k"], m["v"]], [self.xn] * 3, [self.q, self.k, self.v], s)
+                self._group([m["q"], m["k"], m["v"]], [self.xn] * 3, [self.q, self.k, self.v], s)
+            else:
+                # previous layer's x2 + ffnOut (:784), this layer's rmsNorm and the q / k / v
+                # projections (:748-757) in one launch where it applies; the sum goes to the
+                # other residual buffer (the launch's workgroups all read this one)
+                qkv = [m["q"], m["k"], m["v"]]
+                _check(L.jh_rmsnorm_qmatvec_group_dev(3, (_V * 3)(*[q.handle for q in qkv]), P(cur), P(self.proj),
+                                                      P(lw.attn_norm), eps, P(other), P(self.xn),
+                                                      (_V * 3)(P(self.q), P(self.k), P(self.v)), s))
+                cur, other = other, cur
             if lw.bias is not None:  # addInPlace of the projection biases (:758-761)
                 for name, out in (("q", self.q), ("k", self.k), ("v", self.v)):
                     _check(L.jh_add_rows_dev(P(out), P(lw.bias[name]), out.numel(), 1, s))

@@ -136,3 +136,67 @@ def test_rmsnorm_output_projection(qt, rows, cols):
         assert err.max() <= 1e-3
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("cols,shapes", [
+    (4096, [(O.Q4_K, 4096), (O.Q4_K, 1024), (O.Q6_K, 1024)]),   # Llama-3-8B q / k / v of Q4_K_M
+    (2048, [(O.Q4_K, 2048), (O.Q4_K, 256), (O.Q6_K, 256)]),     # TinyLlama
+    (3072, [(O.Q8_0, 3072), (O.Q5_K, 768)]),
+])
+def test_rmsnorm_qkv_group(cols, shapes):
+    """The attention norm fused into the one-shot grouped q / k / v launch
+    (jh_rmsnorm_qmatvec_group_dev): x_out = x + res bit for bit, each output
+    against the unfused composition (jh_rmsnorm_dev, then jh_qmatvec_group_dev;
+    they differ in where the norm's scale is applied and the summation order of
+    mean(h^2): bar 1e-4 with the eps floor) and against the oracle (rmsnorm,
+    then the quantized matvec: the GEMV bar 1e-3)."""
+    import torch
+    L = _lib.load()
+    be = mv.GpuContext.shared(0).create_mat_vec()
+    eps = 1e-5
+    mats = [device_matrix(be, qt, rows, cols, 1820 + i) for i, (qt, rows) in enumerate(shapes)]
+    try:
+        x, res, nw = inputs(cols, 1830)
+        dx, dres, dnw = (torch.from_numpy(a).cuda() for a in (x, res, nw))
+        n = len(mats)
+        xo, xn, xn2 = (torch.full((cols,), float("nan"), device="cuda") for _ in range(3))
+        ys = [torch.full((rows,), float("nan"), device="cuda") for _, rows in shapes]
+        ys2 = [torch.full((rows,), float("nan"), device="cuda") for _, rows in shapes]
+        P = lambda t: ctypes.c_void_p(t.data_ptr())
+        V = ctypes.c_void_p
+        hs = (V * n)(*[m.handle for m in mats])
+        say(f"fused norm + group cols={cols} {shapes}")
+        rc = L.jh_rmsnorm_qmatvec_group_dev(n, hs, P(dx), P(dres), P(dnw), ctypes.c_float(eps), P(xo), P(xn),
+                                            (V * n)(*[P(y) for y in ys]), None)
+        assert rc == 0, _lib.last_error()
+        assert L.jh_rmsnorm_dev(P(dx), P(dres), P(dnw), cols, ctypes.c_float(eps), None, P(xn2), None) == 0
+        assert L.jh_qmatvec_group_dev(n, hs, (V * n)(*[P(xn2)] * n), (V * n)(*[P(y) for y in ys2]), None) == 0
+        torch.cuda.synchronize()
+        h = x + res
+        assert np.array_equal(xo.cpu().numpy(), h)
+        xnr = O.rmsnorm(h, nw, eps)
+        for (qt, rows), m, y, y2 in zip(shapes, mats, ys, ys2):
+            a, b = y.cpu().numpy().astype(np.float64), y2.cpu().numpy().astype(np.float64)
+            raw = m.packed_bytes()
+            absdeq = np.abs(O.dequantize(qt, raw, rows, cols).astype(np.float64))
+            d = np.abs(a - b) / np.maximum(np.abs(b), 1e-3 * (absdeq @ np.abs(xnr.astype(np.float64))))
+            ref = O.matvec(qt, raw, xnr, 0, rows, cols, nthreads=16).astype(np.float64)
+            err = rel_err(a, ref, absdeq, xnr)
+            say(f"  type {qt} {rows}x{cols}: fused vs unfused {d.max():.2e}, vs oracle {err.max():.2e}")
+            assert d.max() <= 1e-4
+            assert err.max() <= 1e-3
+        # without res the unfused path runs (rmsnorm into xn): same outputs as the composition
+        assert L.jh_rmsnorm_qmatvec_group_dev(n, hs, P(dx), None, P(dnw), ctypes.c_float(eps), None, P(xn),
+                                              (V * n)(*[P(y) for y in ys]), None) == 0
+        assert L.jh_rmsnorm_dev(P(dx), None, P(dnw), cols, ctypes.c_float(eps), None, P(xn2), None) == 0
+        assert L.jh_qmatvec_group_dev(n, hs, (V * n)(*[P(xn2)] * n), (V * n)(*[P(y) for y in ys2]), None) == 0
+        torch.cuda.synchronize()
+        for y, y2 in zip(ys, ys2):
+            assert np.array_equal(y.cpu().numpy(), y2.cpu().numpy())
+        # x_out may not alias x
+        rc = L.jh_rmsnorm_qmatvec_group_dev(n, hs, P(dx), P(dres), P(dnw), ctypes.c_float(eps), P(dx), P(xn),
+                                            (V * n)(*[P(y) for y in ys]), None)
+        assert rc == _lib.JH_EINVAL and "alias" in _lib.last_error()
+    finally:
+        for m in mats:
+            m.close()
