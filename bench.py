@@ -610,10 +610,10 @@ def tinyllama_step(torch, stream, steps):
            "ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
            "gemv_ms_per_step": round(gemv_ms, 4), "gemv_tok_s_bound": round(1e3 / gemv_ms, 1),
            "gemv_bytes_per_step": gemv_bytes, "gemv_GB_s": round(gemv_bytes / (gemv_ms * 1e-3) / 1e9, 1),
-           "launches_per_step": cfg.num_layers * 7 + 2,
-           "ops": "rmsnorm(+residual), grouped q/k/v, rope + KV append + GQA (2 kernels), o, "
-                  "residual + rmsnorm + gate/up + silu*up (one launch), down; final residual + rmsnorm + output "
-                  "projection (one launch), position increment"}
+           "launches_per_step": cfg.num_layers * 6 + 3,
+           "ops": "residual + rmsnorm + grouped q/k/v (one launch; layer 0: rmsnorm, then the group), rope + KV "
+                  "append + GQA (2 kernels), o, residual + rmsnorm + gate/up + silu*up (one launch), down; final "
+                  "residual + rmsnorm + output projection (one launch), position increment"}
     del dec
     out["batched"] = tinyllama_batch_step(torch, stream, steps, w, cfg, 32)
     w.close()
