@@ -121,10 +121,10 @@ def test_rope_attention_fused(L, nh, nkv, hd, pos):
     q, k, v = vec(nh * hd, pos + 1), vec(kvd, pos + 2), vec(kvd, pos + 3)
     kc = vec(max_seq * kvd, pos + 4).reshape(max_seq, kvd)
     vc = vec(max_seq * kvd, pos + 5).reshape(max_seq, kvd)
-    dkc, dvc, dq = dev(kc), dev(vc), dev(q)
+    dkc, dvc, dq, dk, dv = dev(kc), dev(vc), dev(q), dev(k), dev(v)  # alive across the call
     out = torch.full((nh * hd,), float("nan"), device="cuda")
     dpos = torch.tensor([pos], dtype=torch.int32, device="cuda")
-    assert L.jh_rope_attention_dev(P(dq), P(dev(k)), P(dev(v)), nh, nkv, hd, P(dpos), max_seq, theta, P(dkc), P(dvc),
+    assert L.jh_rope_attention_dev(P(dq), P(dk), P(dv), nh, nkv, hd, P(dpos), max_seq, theta, P(dkc), P(dvc),
                                    P(out), None) == 0
     kc_ref, vc_ref = kc.copy(), vc.copy()
     kc_ref[pos] = O.rope(k, pos, nkv, hd, theta)
@@ -158,7 +158,8 @@ def test_rope_attention_batched(L, nh, nkv, hd, batch):
     dkc, dvc = dev(kc), dev(vc)
     out = torch.full((batch, nh * hd), float("nan"), device="cuda")
     dpos, dslot = dev(pos, torch.int32), dev(slots, torch.int32)
-    assert L.jh_rope_attention_batched_dev(P(dev(q)), P(dev(k)), P(dev(v)), batch, nh, nkv, hd, P(dpos), P(dslot),
+    dq, dk, dv = dev(q), dev(k), dev(v)  # alive across the call
+    assert L.jh_rope_attention_batched_dev(P(dq), P(dk), P(dv), batch, nh, nkv, hd, P(dpos), P(dslot),
                                            n_slots, max_seq, theta, P(dkc), P(dvc), P(out), None) == 0
     got = out.cpu().numpy()
     for z in range(batch):
@@ -183,7 +184,8 @@ def test_silu_mul_and_pos_increment(L):
     n = 5632
     g, u = vec(n, 7, 4.0), vec(n, 8)
     out = torch.empty(n, device="cuda")
-    assert L.jh_silu_mul_dev(P(dev(g)), P(dev(u)), n, P(out), None) == 0
+    dg, du = dev(g), dev(u)  # alive across the call
+    assert L.jh_silu_mul_dev(P(dg), P(du), n, P(out), None) == 0
     assert np.allclose(out.cpu().numpy(), O.silu_mul(g, u), rtol=2e-6, atol=1e-7)
     pos = torch.tensor([41], dtype=torch.int32, device="cuda")
     assert L.jh_pos_increment_dev(P(pos), 1, None) == 0
