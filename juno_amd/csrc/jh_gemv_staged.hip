@@ -226,6 +226,12 @@ template <int N> struct XLimbs {
 #pragma unroll
         for (int k = 0; k < kLimbs; k++) h[k] = sdot4(q, b[k][i], h[k]);
     }
+    // the same, starting the sums (the three-operand form with a zero addend: the
+    // compiler would otherwise zero each sum with a move and then accumulate)
+    __device__ __forceinline__ void dot_first(uint32_t q, int i, int (&h)[kLimbs]) const {
+#pragma unroll
+        for (int k = 0; k < kLimbs; k++) asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(h[k]) : "v"(q), "v"(b[k][i]));
+    }
 };
 
 // Per-lane conversion (column tiles, no shared image): the group's digit
@@ -353,8 +359,13 @@ __device__ __forceinline__ float kq_block_dot(const XRegs<12> &x, const uint8_t 
         kq_quants<Q5>(p, g, lo, hi);
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            x.dot(lo[k], k, d0);  // quants 0..31: non-negative signed bytes
-            x.dot(hi[k], 8 + k, d1);
+            if (k == 0) {
+                x.dot_first(lo[k], k, d0);  // quants 0..31: non-negative signed bytes
+                x.dot_first(hi[k], 8 + k, d1);
+            } else {
+                x.dot(lo[k], k, d0);
+                x.dot(hi[k], 8 + k, d1);
+            }
         }
     }
     const float s0 = x.a0 * limbs(d0), s1 = x.a1 * limbs(d1);
@@ -417,7 +428,10 @@ __device__ __forceinline__ float block_dot(const XRegs<14> &x, const uint8_t *p,
         uint32_t q[4];
         q6_quads(lds_word(wa, sh, k), lds_word(wb, sh, k), lds_word(wq, sh, k), q);
 #pragma unroll
-        for (int j = 0; j < 4; j++) x.dot(q[j], 4 * j + k, acc[j]);
+        for (int j = 0; j < 4; j++) {
+            if (k == 0) x.dot_first(q[j], 4 * j + k, acc[j]);
+            else x.dot(q[j], 4 * j + k, acc[j]);
+        }
     }
     float sj[4];
 #pragma unroll
@@ -445,7 +459,10 @@ __device__ __forceinline__ float block_dot(const XRegs<8> &x, const uint8_t *p, 
     auto quants = [&](int k) { return __builtin_amdgcn_alignbyte(w[k + 1 + (sh >> 1)], w[k + (sh >> 1)], (sh + 2) & 3); };
     int h[kLimbs] = {};
 #pragma unroll
-    for (int k = 0; k < 8; k++) x.dot(quants(k), k, h);
+    for (int k = 0; k < 8; k++) {
+        if (k == 0) x.dot_first(quants(k), k, h);
+        else x.dot(quants(k), k, h);
+    }
     const float s = x.a * limbs(h);
     return d * s;
 }
