@@ -116,19 +116,22 @@ __device__ __forceinline__ float x_scale(float mx, int s) { return mx > 0.f ? ld
 struct Limbs {
     uint32_t b[kLimbs];  // b[0]: the top digit (256^3)
 };
+// The 4 x 4 byte transpose takes eight byte permutes (v_perm_b32: selector
+// bytes 0..3 pick bytes of the second operand, 4..7 of the first).
 __device__ __forceinline__ Limbs to_limbs(float4 v, int s) {
     const float e[4] = {v.x, v.y, v.z, v.w};
+    uint32_t u[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) u[j] = (uint32_t)(int)rintf(ldexpf(e[j], s)) + 0x80808080u;  // |xi| < 2^30
+    const uint32_t lo01 = __builtin_amdgcn_perm(u[1], u[0], 0x05010400u);  // u0.b0 u1.b0 u0.b1 u1.b1
+    const uint32_t hi01 = __builtin_amdgcn_perm(u[1], u[0], 0x07030602u);  // u0.b2 u1.b2 u0.b3 u1.b3
+    const uint32_t lo23 = __builtin_amdgcn_perm(u[3], u[2], 0x05010400u);
+    const uint32_t hi23 = __builtin_amdgcn_perm(u[3], u[2], 0x07030602u);
     Limbs r;
-#pragma unroll
-    for (int k = 0; k < kLimbs; k++) r.b[k] = 0u;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t u = (uint32_t)(int)rintf(ldexpf(e[j], s)) + 0x80808080u;  // |xi| < 2^30
-#pragma unroll
-        for (int k = 0; k < kLimbs; k++) r.b[k] |= ((u >> (24 - 8 * k)) & 0xFFu) << (8 * j);
-    }
-#pragma unroll
-    for (int k = 0; k < kLimbs; k++) r.b[k] ^= 0x80808080u;
+    r.b[0] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u) ^ 0x80808080u;  // byte 3 of u0..u3
+    r.b[1] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;  // byte 2
+    r.b[2] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;  // byte 1
+    r.b[3] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;  // byte 0
     return r;
 }
 
@@ -569,7 +572,8 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     //    wave converts (up to 16 blocks over 4 waves for one column tile, up to
     //    64 over 8-16 waves for column tiles), all issued here rather than one
     //    round trip per block; otherwise this lane's own columns
-    constexpr int NXS = ((NW >= 8 ? 64 : 16) + NW - 1) / NW;  // image blocks each wave converts
+    // image blocks each wave converts: one column tile has at most 16 blocks
+    constexpr int NXS = (((DYN || NORM || NW < 8) ? 16 : 64) + NW - 1) / NW;
     constexpr int NX = SX ? NXS : (T == 8 ? 8 : 16);
     float4 xv[NX];
     float4 rv[NORM ? NXS : 1], nwv[NORM ? NXS : 1];
@@ -615,7 +619,12 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
                 if (lane + 64 * k < F::CH) dst[i * F::CH + lane + 64 * k] = v[i][k];
     };
     if constexpr (DYN) grp = grp < gend ? grp : ngroups;  // a range shorter than the waves: nothing to do
-    issue(grp);
+    // The first weight loads: per-lane x issues them now; a shared image issues
+    // them after its barrier.  A CU accepts only so many loads at a time, so the
+    // waves' first bursts issue in turns (the last third of a 12-wave workgroup
+    // ~1 us after the first); issued before the conversion, they held each
+    // wave's share of it, and with it the barrier, until the wave's turn came.
+    if constexpr (!shared_x) issue(grp);
     asm volatile("" ::: "memory");
 
     // 3. x into registers
@@ -654,6 +663,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
         for (int bx = wave + NW * NXS; bx < nblk; bx += NW)
             x_quant_block<F::G>(im, bx, x_load4(args.x, args.cols, bx * 256 + lane * 4));
         __syncthreads();
+        issue(grp);
         xr.load(im, b, sub, act);
     } else {
 #pragma unroll
