@@ -142,6 +142,8 @@ def test_rmsnorm_output_projection(qt, rows, cols):
     (4096, [(O.Q4_K, 4096), (O.Q4_K, 1024), (O.Q6_K, 1024)]),   # Llama-3-8B q / k / v of Q4_K_M
     (2048, [(O.Q4_K, 2048), (O.Q4_K, 256), (O.Q6_K, 256)]),     # TinyLlama
     (3072, [(O.Q8_0, 3072), (O.Q5_K, 768)]),
+    (8192, [(O.Q4_K, 512), (O.Q8_0, 256)]),                     # the widest input the LDS image takes
+    (14336, [(O.Q6_K, 300)]),                                    # wider: the unfused pair
 ])
 def test_rmsnorm_qkv_group(cols, shapes):
     """The attention norm fused into the one-shot grouped q / k / v launch
