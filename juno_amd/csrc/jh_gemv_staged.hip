@@ -799,8 +799,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_staged(StagedArgs args) {
     gemv_staged_body<T, R, SX, NW, NORM, DYN>(args);
 }
 
-// One-column-tile rows take one 12-wave workgroup per CU whose waves claim row
-// groups (DYN), unless JUNO_STAGED_DYN=0: then 4-wave workgroups, up to 3 per CU,
+// One-column-tile rows take one workgroup per CU (16 waves of one row, or 12 of
+// two for the SwiGLU pairing) whose waves claim row groups (DYN), unless JUNO_STAGED_DYN=0: then 4-wave workgroups, up to 3 per CU,
 // with equal static shares (JUNO_STAGED_NW = 8 or 12 widens them), for A/B runs.
 // Measured with per-workgroup timestamps on the static layout: on the 8B lm_head
 // the first workgroup on each CU ended at ~53 us, the second at ~62, the third at
@@ -896,7 +896,10 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
     const int ngroups = (sa.nrows + R - 1) / R;
     if (sa.norm_w) {  // the rmsnorm prologue needs the shared image and every block in one pass of the waves
         if (sa.gw != 1 || nblk > 16) return hipErrorNotSupported;
-        if (staged_dyn()) return launch_staged_nw<T, R, true, 12, true, true>(sa, nblk, ngroups, s);
+        if (staged_dyn()) {
+            if (R == 1) return launch_staged_nw<T, 1, true, 16, true, true>(sa, nblk, ngroups, s);
+            return launch_staged_nw<T, R, true, 12, true, true>(sa, nblk, ngroups, s);
+        }
         return launch_staged_nw<T, R, true, 4, true>(sa, nblk, ngroups, s);
     }
     if (sa.gw != 1) {
@@ -910,7 +913,11 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
         if (e != hipErrorNotSupported) return e;
         return launch_staged_nw<T, R, false, 4>(sa, nblk, ngroups, s);
     }
-    if (staged_dyn()) return launch_staged_nw<T, R, true, 12, false, true>(sa, nblk, ngroups, s);
+    if (staged_dyn()) {
+        // one row per group: 16 waves (what fits 128 VGPRs); two (the SwiGLU pairing): 12
+        if (R == 1) return launch_staged_nw<T, 1, true, 16, false, true>(sa, nblk, ngroups, s);
+        return launch_staged_nw<T, R, true, 12, false, true>(sa, nblk, ngroups, s);
+    }
     switch (staged_waves()) {
     case 8: return launch_staged_nw<T, R, true, 8>(sa, nblk, ngroups, s);
     case 12: return launch_staged_nw<T, R, true, 12>(sa, nblk, ngroups, s);
@@ -949,9 +956,9 @@ static hipError_t launch_staged_r(const StagedArgs &sa, int R, hipStream_t s) {
     }
 }
 
-// Rows per group: 2, or 1 for column-tiled rows (with the shared x image, 16 waves of
-// one row each; 8B ffn_down 20.2 -> 19.3 us, TinyLlama 10.1 -> 7.9 us, Phi-3 Q8_0
-// 13.3 -> 10.1 us).
+// Column-tiled rows (more blocks than one wave's tile): one row per group, 16 waves
+// sharing the x image (8B ffn_down 20.2 -> 19.3 us, TinyLlama 10.1 -> 7.9 us,
+// Phi-3 Q8_0 13.3 -> 10.1 us against two rows and per-lane x).
 static bool staged_wide(int type, int nb) {
     switch (type) {
     case 12: return nb > Fmt<12>::TBMAX;
@@ -962,7 +969,12 @@ static bool staged_wide(int type, int nb) {
     }
 }
 static hipError_t launch_staged_any(const StagedArgs &sa, int type, hipStream_t s) {
-    const int R = staged_rows(staged_wide(type, sa.nb) ? 1 : 2);
+    // One row per group unless the SwiGLU pairing needs two.  With one row, 16
+    // waves fit a CU (128 VGPRs each) against 12 waves of two rows: the same bytes
+    // in flight, but groups half as long, so the claims balance the waves more
+    // finely (same box: [gate, up] 17.4 -> 16.3 us, lm_head 75.2 -> 72.2 us, the
+    // B = 1 step 1.644 -> 1.617 ms).
+    const int R = staged_rows(staged_wide(type, sa.nb) || !sa.swiglu ? 1 : 2);
     switch (type) {
     case 12: return launch_staged_r<12>(sa, R, s);
     case 13: return launch_staged_r<13>(sa, R, s);
