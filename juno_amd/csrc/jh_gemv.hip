@@ -15,10 +15,22 @@
 // each sub-block is folded as  scale * sum(q*x) - min * sum(x)  (fp32 FMAs),
 // which is the same sum in another order; the difference is order-of-
 // summation rounding only (bar: max rel-err 1e-3 against the Java path).
+// Quants with an offset (Q6_K u - 32, Q3_K q - 4) or a sign (Q8_0) enter as signed values
+// (a signed bit-field extract of the offset-flipped field), never as
+// sum(u*x) - 32 * sum(x): that difference cancels in fp32 when x has an
+// outlier over a zero weight.
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
 
 namespace jh {
+
+// The signed W-bit field of w at bit off, by shifts (the compiler treated the
+// result of __builtin_amdgcn_sbfe as non-negative and converted it to float
+// as unsigned).
+template <int W>
+__device__ __forceinline__ int sfield(uint32_t w, int off) {
+    return (int)(w << (32 - W - off)) >> (32 - W);
+}
 
 // ---------------------------------------------------------------- Q4_K / Q5_K
 // Lane (kb, ch): block b = step*8 + kb, 16-byte qs chunk ch of that block.
@@ -173,16 +185,6 @@ __device__ __forceinline__ void gemv_q6k_body(int wg, const uint8_t *__restrict_
         }
     };
     auto compute = [&](const Step &t) {
-        float sx[B][4];
-#pragma unroll
-        for (int j = 0; j < B; j++)
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                float s = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) s += t.xv[j][k][e];
-                sx[j][k] = s;
-            }
 #pragma unroll
         for (int i = 0; i < R; i++) {
             const float d = half_bits_to_float(t.dw[i]);
@@ -200,10 +202,11 @@ __device__ __forceinline__ void gemv_q6k_body(int wg, const uint8_t *__restrict_
             for (int tt = 0; tt < 2; tt++) {
                 const uint32_t a = tt ? t.qa[i].y : t.qa[i].x, c = tt ? t.qb[i].y : t.qb[i].x,
                                e = tt ? t.qh[i].y : t.qh[i].x;
-                u[0][tt] = (a & 0x0F0F0F0Fu) | ((e << 4) & 0x30303030u);
-                u[1][tt] = (c & 0x0F0F0F0Fu) | ((e << 2) & 0x30303030u);
-                u[2][tt] = ((a >> 4) & 0x0F0F0F0Fu) | (e & 0x30303030u);
-                u[3][tt] = ((c >> 4) & 0x0F0F0F0Fu) | ((e >> 2) & 0x30303030u);
+                // 6-bit u with bit 5 flipped: as a signed 6-bit field it is u - 32
+                u[0][tt] = ((a & 0x0F0F0F0Fu) | ((e << 4) & 0x30303030u)) ^ 0x20202020u;
+                u[1][tt] = ((c & 0x0F0F0F0Fu) | ((e << 2) & 0x30303030u)) ^ 0x20202020u;
+                u[2][tt] = (((a >> 4) & 0x0F0F0F0Fu) | (e & 0x30303030u)) ^ 0x20202020u;
+                u[3][tt] = (((c >> 4) & 0x0F0F0F0Fu) | ((e >> 2) & 0x30303030u)) ^ 0x20202020u;
             }
 #pragma unroll
             for (int j = 0; j < B; j++) {
@@ -212,10 +215,9 @@ __device__ __forceinline__ void gemv_q6k_body(int wg, const uint8_t *__restrict_
                 for (int k = 0; k < 4; k++) {
                     float dot = 0.f;
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        dot = fmaf((float)byte_of(u[k][e >> 2], e & 3), t.xv[j][k][e], dot);
-                    // q = u - 32
-                    a = fmaf(dk[k], fmaf(-32.f, sx[j][k], dot), a);
+                    for (int e = 0; e < 8; e++)  // q = u - 32
+                        dot = fmaf((float)sfield<6>(u[k][e >> 2], 8 * (e & 3)), t.xv[j][k][e], dot);
+                    a = fmaf(dk[k], dot, a);
                 }
                 acc[i][j] = a;
             }
@@ -341,7 +343,7 @@ __device__ __forceinline__ void gemv_q2k_body(int wg, const uint8_t *__restrict_
 // Lane (kb, ch): block b = step*8 + kb; half h = ch/4, r = (ch/2)&1, l0 = 8*(ch&1).
 // Elements h*128 + 32j + 16r + l (j = 0..3, l in [l0, l0+8)) take the 2 bits at
 // shift 2j of qs[32h + 16r + l], bit 4h + j of hmask[16r + l] and the signed
-// scale sc[8h + 2j + r]: w = (d*sc) * (q - 4), folded as d*sc*(sum(q*x) - 4*sum(x)).
+// scale sc[8h + 2j + r]: w = (d*sc) * (q - 4), folded as d*sc*sum((q - 4)*x).
 // Blocks are 2-byte aligned (110 bytes).
 template <int R, int B>
 __device__ __forceinline__ void gemv_q3k_body(int wg, const uint8_t *__restrict__ W, size_t pitch, int nb,
@@ -372,7 +374,7 @@ __device__ __forceinline__ void gemv_q3k_body(int wg, const uint8_t *__restrict_
             a01[i] = load8_a2(bp + 96);   // scale words aux0, aux1
             a2d[i] = load8_a2(bp + 104);  // aux2, then d in the low half of .y
         }
-        float xv[B][4][8], sx[B][4];
+        float xv[B][4][8];
 #pragma unroll
         for (int j = 0; j < B; j++) {
             const float *xp = X + (size_t)j * ldx + b * 256 + h * 128 + 16 * r + l0;
@@ -381,10 +383,6 @@ __device__ __forceinline__ void gemv_q3k_body(int wg, const uint8_t *__restrict_
                 float4 a = load_f4(xp + 32 * k), c = load_f4(xp + 32 * k + 4);
                 xv[j][k][0] = a.x; xv[j][k][1] = a.y; xv[j][k][2] = a.z; xv[j][k][3] = a.w;
                 xv[j][k][4] = c.x; xv[j][k][5] = c.y; xv[j][k][6] = c.z; xv[j][k][7] = c.w;
-                float s = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; e++) s += xv[j][k][e];
-                sx[j][k] = s;
             }
         }
 #pragma unroll
@@ -401,8 +399,9 @@ __device__ __forceinline__ void gemv_q3k_body(int wg, const uint8_t *__restrict_
                 const int s6 = (int)byte_of(k < 2 ? ua : ub, 2 * (k & 1) + r) - 32;
                 dsc[k] = d * (float)s6;
                 const int hb = 4 * h + k;
-                u[k][0] = ((q[i].x >> (2 * k)) & 0x03030303u) | (((hm[i].x >> hb) & 0x01010101u) << 2);
-                u[k][1] = ((q[i].y >> (2 * k)) & 0x03030303u) | (((hm[i].y >> hb) & 0x01010101u) << 2);
+                // 3-bit q with bit 2 flipped: as a signed 3-bit field it is q - 4
+                u[k][0] = (((q[i].x >> (2 * k)) & 0x03030303u) | (((hm[i].x >> hb) & 0x01010101u) << 2)) ^ 0x04040404u;
+                u[k][1] = (((q[i].y >> (2 * k)) & 0x03030303u) | (((hm[i].y >> hb) & 0x01010101u) << 2)) ^ 0x04040404u;
             }
 #pragma unroll
             for (int j = 0; j < B; j++) {
@@ -412,8 +411,8 @@ __device__ __forceinline__ void gemv_q3k_body(int wg, const uint8_t *__restrict_
                     float dot = 0.f;
 #pragma unroll
                     for (int e = 0; e < 8; e++)
-                        dot = fmaf((float)byte_of(u[k][e >> 2], e & 3), xv[j][k][e], dot);
-                    a = fmaf(dsc[k], fmaf(-4.f, sx[j][k], dot), a);
+                        dot = fmaf((float)sfield<3>(u[k][e >> 2], 8 * (e & 3)), xv[j][k][e], dot);
+                    a = fmaf(dsc[k], dot, a);
                 }
                 acc[i][j] = a;
             }
@@ -469,8 +468,7 @@ __device__ __forceinline__ void gemv_q8_0_body(int wg, const uint8_t *__restrict
 #pragma unroll
             for (int k = 0; k < 8; k++) {
                 const uint32_t lo = mis ? v[k + 1] : v[k], hi = mis ? v[k + 2] : v[k + 1];
-                // flip the sign bits: byte value u = q + 128
-                q[i][k] = __builtin_amdgcn_alignbyte(hi, lo, mis ? 0u : 2u) ^ 0x80808080u;
+                q[i][k] = __builtin_amdgcn_alignbyte(hi, lo, mis ? 0u : 2u);
             }
         }
 #pragma unroll
@@ -482,15 +480,12 @@ __device__ __forceinline__ void gemv_q8_0_body(int wg, const uint8_t *__restrict
                 float4 a = load_f4(xp + 4 * k);
                 xv[4 * k] = a.x; xv[4 * k + 1] = a.y; xv[4 * k + 2] = a.z; xv[4 * k + 3] = a.w;
             }
-            float s = 0.f;
-#pragma unroll
-            for (int k = 0; k < 32; k++) s += xv[k];
 #pragma unroll
             for (int i = 0; i < R; i++) {
-                float dot = 0.f;
+                float dot = 0.f;  // q as signed bytes (sign-extending byte selects of the convert)
 #pragma unroll
-                for (int k = 0; k < 32; k++) dot = fmaf((float)byte_of(q[i][k >> 2], k & 3), xv[k], dot);
-                acc[i][j] = fmaf(dsc[i], fmaf(-128.f, s, dot), acc[i][j]);
+                for (int k = 0; k < 32; k++) dot = fmaf((float)sfield<8>(q[i][k >> 2], 8 * (k & 3)), xv[k], dot);
+                acc[i][j] = fmaf(dsc[i], dot, acc[i][j]);
             }
         }
     }

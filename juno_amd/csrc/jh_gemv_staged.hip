@@ -31,7 +31,11 @@
 // summation order is rounding x * 2^s to an integer below 2^30 in magnitude,
 // with one s per quant sub-block of x: exact for elements within 2^6 of the
 // sub-block's maximum |x|, within 2^-18 of themselves down to 2^-12 of it,
-// an absolute error of at most 2^-31 of that maximum below.
+// an absolute error of at most 2^-31 of that maximum below.  When that
+// rounding is not small against a sub-block's other elements (one outlier
+// setting the scale of many small elements), the launch takes an exact fp32
+// path instead of the walk (staged_exact below).
+#include "jh_dequant.hpp"
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
 
@@ -107,9 +111,35 @@ __device__ __forceinline__ float amax4(float4 v) {
     return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 // The shift s of a group with maximum |x| = mx (|x * 2^s| < 2^30), and its
-// scale 2^-s (0 for an all-zero group, so that it contributes nothing).
-__device__ __forceinline__ int x_shift(float mx) { return mx > 0.f ? 30 - __builtin_amdgcn_frexp_expf(mx) : 0; }
+// scale 2^-s (0 for an all-zero group, so that it contributes nothing).  s is
+// at most 149, so that 2^-s is still an fp32 value (the smallest subnormal):
+// an integer times it is then exact below 2^24 and rounded once above, and a
+// group whose maximum is below 2^-119 keeps fewer than 30 bits, all of them
+// above the fp32 products' own rounding (2^-150) there.
+__device__ __forceinline__ int x_shift(float mx) {
+    return mx > 0.f ? min(30 - __builtin_amdgcn_frexp_expf(mx), 149) : 0;
+}
 __device__ __forceinline__ float x_scale(float mx, int s) { return mx > 0.f ? ldexpf(1.f, -s) : 0.f; }
+
+// The residual.  Rounding x * 2^s to an integer xi leaves r = x - 2^-s xi,
+// |r| <= 2^-(s+1) <= 2^-30 max|x|, exactly representable (Sterbenz: xi 2^-s
+// is within a factor 2 of x whenever xi != 0).  It matters only when one
+// large element sets the scale of many much smaller ones: when the mean |x|
+// of the group's other elements is below 2^-10 of its maximum (and not 0:
+// a lone nonzero element is exact).  Otherwise each element's rounding error
+// is at most 2^-19 of that mean.  A normal-range x never meets this (channels
+// at 300x do not); x with a 1e4 outlier among 1e-2 elements does.  The test is
+// a property of x alone, so every workgroup of a launch reaches the same
+// answer.  When any group meets it, the launch computes sum deq(w) * x with
+// the fp32 x itself instead (staged_exact): x is then used exactly, as the
+// reference uses it.
+// mx = max |x|, sa = sum |x| over the group.
+template <int G>
+__device__ __forceinline__ bool residual_matters(float mx, float sa) {
+    const float rest = sa - mx;
+    return rest > 0.f && rest * 1024.f < (float)(G - 1) * mx;
+}
+__device__ __forceinline__ float asum4(float4 v) { return (fabsf(v.x) + fabsf(v.y)) + (fabsf(v.z) + fabsf(v.w)); }
 
 // The digit dwords of 4 consecutive x values: dword k holds digit k of value
 // j in byte j (the bytes of xi + 0x80808080, each less 128).
@@ -155,6 +185,15 @@ __device__ __forceinline__ float group_red(float v) {
     if (G == 32) v = dpp_red<0x141, MAX>(v);   // row_half_mirror
     return v;
 }
+// sum of v over the lanes of a group (as group_red)
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+    if (G == 32)
+        v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+    return v;
+}
 
 // Rows of one column tile (gw == 1) need all of x in every wave of the
 // workgroup: there the waves convert x once, cooperatively, into an LDS image,
@@ -172,13 +211,24 @@ struct XImage {
     static __host__ __device__ size_t bytes(int nblk) { return (size_t)nblk * (256 * kLimbs + 64 + 64); }
 };
 
+// LDS of a staged workgroup: [image (shared x)][row-group buffers][ring
+// partials][ring arrival / release counters]; then the claim counter and the
+// per-wave residual flags.
+constexpr int kRing = 4;  // cells per slot of the column-tile ring (a power of two)
+__host__ __device__ constexpr size_t staged_front(bool sx, int nblk, int nw, int r, int ch) {
+    return (sx ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)nw * r * ch * 16 +
+           (size_t)kRing * nw * r * 4 + 2 * kRing * nw * 4;
+}
+
 // Block b of 256 columns into the image, one wave: the lane holds columns
 // 256 b + 4 lane .. +4.
+// Returns whether the lane's group needs the exact path.
 template <int G>
-__device__ __forceinline__ void x_quant_block(const XImage &im, int b, float4 v) {
+__device__ __forceinline__ bool x_quant_block(const XImage &im, int b, float4 v) {
     const int lane = threadIdx.x & 63;
     if (b * 256 + lane * 4 >= im.cols) v = make_float4(0.f, 0.f, 0.f, 0.f);
     const float mx = group_red<G, true>(amax4(v));
+    const bool need = residual_matters<G>(mx, group_sum<G>(asum4(v)));
     const int s = x_shift(mx);
     const Limbs l = to_limbs(v, s);
 #pragma unroll
@@ -187,6 +237,7 @@ __device__ __forceinline__ void x_quant_block(const XImage &im, int b, float4 v)
     // sums over 4 lanes (16 columns) with DPP (quad_perm) rather than LDS permutes
     const float xs = quad_sum((v.x + v.y) + (v.z + v.w));
     if ((lane & 3) == 0) im.xs16()[b * 16 + (lane >> 2)] = xs;
+    return need;
 }
 
 // sum_k 256^(3-k) h_k of the four digit dot products, in fp32: two exact
@@ -238,17 +289,23 @@ template <int N> struct XLimbs {
 };
 
 // Per-lane conversion (column tiles, no shared image): the group's digit
-// dwords for n float4s v[0..n) starting at register index at, and its scale.
+// dwords for n float4s v[at..at+n), and its scale; need is or-ed with whether
+// the group needs the exact path.
 template <int N, int M>
-__device__ __forceinline__ float convert_group(XLimbs<N> &x, const float4 (&v)[M], int at, int n) {
+__device__ __forceinline__ float convert_group(XLimbs<N> &x, const float4 (&v)[M], int at, int n, bool &need) {
     float mx = 0.f;
 #pragma unroll
     for (int k = 0; k < M; k++)
         if (k >= at && k < at + n) mx = fmaxf(mx, amax4(v[k]));
     const int s = x_shift(mx);
+    float sa = 0.f;
 #pragma unroll
     for (int k = 0; k < M; k++)
-        if (k >= at && k < at + n) x.set(k, to_limbs(v[k], s));
+        if (k >= at && k < at + n) {
+            sa += asum4(v[k]);
+            x.set(k, to_limbs(v[k], s));
+        }
+    need |= n == 8 ? residual_matters<32>(mx, sa) : residual_matters<16>(mx, sa);
     return x_scale(mx, s);
 }
 
@@ -266,18 +323,20 @@ template <> struct XRegs<12> : XLimbs<16> {
         xs0 = act ? s.x + s.y : 0.f;
         xs1 = act ? s.z + s.w : 0.f;
     }
-    __device__ void convert(const float4 (&v)[16], bool act) {
+    __device__ bool convert(const float4 (&v)[16], bool act) {
         float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             const float s = (v[k].x + v[k].y) + (v[k].z + v[k].w);
             if (k < 8) s0 += s; else s1 += s;
         }
-        const float c0 = convert_group(*this, v, 0, 8), c1 = convert_group(*this, v, 8, 8);
+        bool need = false;
+        const float c0 = convert_group(*this, v, 0, 8, need), c1 = convert_group(*this, v, 8, 8, need);
         a0 = act ? c0 : 0.f;
         a1 = act ? c1 : 0.f;
         xs0 = act ? s0 : 0.f;
         xs1 = act ? s1 : 0.f;
+        return need;
     }
 };
 
@@ -300,12 +359,14 @@ template <> struct XRegs<14> : XLimbs<16> {
             a[k] = act ? im.scale()[c / 16] : 0.f;
         }
     }
-    __device__ void convert(const float4 (&v)[16], bool act) {
+    __device__ bool convert(const float4 (&v)[16], bool act) {
+        bool need = false;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float c = convert_group(*this, v, 4 * r, 4);
+            const float c = convert_group(*this, v, 4 * r, 4, need);
             a[r] = act ? c : 0.f;
         }
+        return need;
     }
 };
 
@@ -317,9 +378,11 @@ template <> struct XRegs<8> : XLimbs<8> {
         load_run(im, b * 8, 0, 8);
         a = act ? im.scale()[b * 2] : 0.f;
     }
-    __device__ void convert(const float4 (&v)[8], bool act) {
-        const float c = convert_group(*this, v, 0, 8);
+    __device__ bool convert(const float4 (&v)[8], bool act) {
+        bool need = false;
+        const float c = convert_group(*this, v, 0, 8, need);
         a = act ? c : 0.f;
+        return need;
     }
 };
 
@@ -498,8 +561,6 @@ struct StagedArgs {
 // SwiGLU pairing: virtual row v is row v / 2 of gate (v even) or up (v odd),
 // so that a row group (R even) holds both halves of its outputs.
 
-// cells per slot of the column-tile ring (a power of two)
-constexpr int kRing = 4;
 
 __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
     int p = 0;
@@ -507,6 +568,51 @@ __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
     for (int i = 1; i < kMaxStagedGroup; i++)
         if (i < a.np && v >= a.cum[i]) p = i;
     return p;
+}
+
+// The exact path: launches whose x needs it (residual_matters) take it instead of
+// the walk, every workgroup alike.  One wave per output (a row, or a gate / up
+// pair under the SwiGLU pairing), rows strided over the grid's waves; each lane
+// sums deq(w) * x over the quant units lane, lane + 64, .. with the fp32 x
+// itself (NORM: formed as the prologue forms it), then the wave adds the lanes'
+// sums.  That is the reference's term (LlamaTransformerHandler.java:1457-1460)
+// in another summation order, at a fraction of the walk's speed: it is the
+// path for x with one outlier among many much smaller elements, which the
+// walk's 30-bit fixed point per sub-block does not carry to the GEMV bar.
+template <int T, bool NORM>
+__device__ __forceinline__ void staged_exact(const StagedArgs &args, float nscale) {
+    constexpr int G = Fmt<T>::G;
+    const int lane = threadIdx.x & 63;
+    // the wave's index, uniform (readfirstlane): rows and matrices are then chosen
+    // with scalar loads of the arguments, as the walk chooses them
+    const int waves = (int)(blockDim.x >> 6);
+    const int gwave = __builtin_amdgcn_readfirstlane((int)blockIdx.x * waves + (int)(threadIdx.x >> 6));
+    const int units = args.cols / G;
+    auto xat = [&](int64_t c) {
+        return NORM ? (args.norm_w[c] * (args.x[c] + args.res[c])) * nscale : args.x[c];
+    };
+    auto row_dot = [&](int vr) {
+        const int p = args.swiglu ? (vr & 1) : staged_problem(args, vr);
+        const int rr = args.swiglu ? (vr >> 1) : vr - args.cum[p];
+        const uint8_t *row = args.w[p] + (size_t)(args.row0[p] + rr) * args.pitch;
+        float acc = 0.f;
+        for (int u = lane; u < units; u += 64)
+            deq_unit<T, false>(row, u, [&](int64_t c, float w) { acc = fmaf(w, xat(c), acc); });
+        return wave_sum(acc);
+    };
+    const int nout = args.swiglu ? args.nrows / 2 : args.nrows;
+    for (int o = gwave; o < nout; o += (int)gridDim.x * waves) {
+        if (args.swiglu) {
+            const float g = row_dot(2 * o), u = row_dot(2 * o + 1);
+            if (lane == 0) args.swiglu[o] = silu_times(g, u);
+        } else {
+            const float v = row_dot(o);
+            if (lane == 0) {
+                const int p = staged_problem(args, o);
+                args.y[p][o - args.cum[p]] = v;
+            }
+        }
+    }
 }
 
 // SX: one column tile, x shared through an LDS image; NW: waves per workgroup;
@@ -536,6 +642,8 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     float *part = reinterpret_cast<float *>(stage + NW * R * F::CH);
     int *ring_arr = reinterpret_cast<int *>(part + kRing * NW * R);  // [slot][cell]: arrivals
     int *ring_done = ring_arr + kRing * NW;                            // [slot][cell]: uses finished
+    int *claim = reinterpret_cast<int *>(lds + staged_front(SX, nblk, NW, R, F::CH));  // DYN: next group
+    int *xneed = claim + 1;  // [NW]: x needs the exact path
 
     const int slots = NW / gw;  // row groups processed side by side by one workgroup
     const int tile = wave % gw, slot = wave / gw;
@@ -546,7 +654,6 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     const int gper = ngroups / (int)gridDim.x, gext = ngroups - gper * (int)gridDim.x;
     const int gbeg = (int)blockIdx.x * gper + min((int)blockIdx.x, gext);
     const int gend = gbeg + gper + ((int)blockIdx.x < gext ? 1 : 0);
-    int *claim = ring_done + kRing * NW;  // DYN: the next unclaimed group
     // the ring's counters start at zero; read only after the barrier of the x prologue
     if (SX && (int)threadIdx.x < 2 * kRing * NW) ring_arr[threadIdx.x] = 0;
     if constexpr (DYN) {
@@ -602,7 +709,8 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
 #pragma unroll
         for (int i = 0; i < R; i++) {
             const int vr = min(r0 + i, nrows - 1);
-            const int p = args.swiglu ? (vr & 1) : staged_problem(args, vr);
+            // uniform over the wave: the matrix is chosen with scalar loads
+            const int p = __builtin_amdgcn_readfirstlane(args.swiglu ? (vr & 1) : staged_problem(args, vr));
             const int rr = args.swiglu ? (vr >> 1) : vr - args.cum[p];
             const size_t off = (size_t)(args.row0[p] + rr) * pitch + tile_off;
             start[i] = (int)(off & 15);
@@ -629,6 +737,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
 
     // 3. x into registers
     XRegs<T> xr;
+    float nscale = 1.f;  // NORM: the rmsnorm scale
     if constexpr (NORM) {
         // h = x + res and its sum of squares: per lane, then over the wave (DPP),
         // then over the waves in wave order through LDS (the part area, unused
@@ -651,24 +760,39 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
 #pragma unroll
         for (int w = 0; w < NW; w++) tot += part[w];
         const float scale = 1.f / (float)sqrt((double)(tot / (float)args.cols + args.eps));
+        nscale = scale;
 #pragma unroll
         for (int k = 0; k < NXS; k++)
             xv[k] = make_float4(nwv[k].x * xv[k].x * scale, nwv[k].y * xv[k].y * scale, nwv[k].z * xv[k].z * scale,
                                 nwv[k].w * xv[k].w * scale);
     }
     if constexpr (shared_x) {
+        // each wave's flag: whether a group it converted needs the exact path
+        bool need = false;
 #pragma unroll
         for (int k = 0; k < NXS; k++)
-            if (wave + NW * k < nblk) x_quant_block<F::G>(im, wave + NW * k, xv[k]);
+            if (wave + NW * k < nblk) need |= x_quant_block<F::G>(im, wave + NW * k, xv[k]);
         for (int bx = wave + NW * NXS; bx < nblk; bx += NW)
-            x_quant_block<F::G>(im, bx, x_load4(args.x, args.cols, bx * 256 + lane * 4));
+            need |= x_quant_block<F::G>(im, bx, x_load4(args.x, args.cols, bx * 256 + lane * 4));
+        const bool wneed = __builtin_amdgcn_ballot_w64(need) != 0;  // over all lanes of the wave
+        if (lane == 0) xneed[wave] = wneed;
         __syncthreads();
+        int anyneed = 0;
+#pragma unroll
+        for (int w = 0; w < NW; w++) anyneed |= xneed[w];
+        if (__builtin_amdgcn_readfirstlane(anyneed)) {  // uniform over the workgroup; see residual_matters
+            staged_exact<T, NORM>(args, nscale);
+            return;
+        }
         issue(grp);
         xr.load(im, b, sub, act);
     } else {
 #pragma unroll
         for (int k = 0; k < NX; k++) xv[k] = x_mask4(xv[k], args.cols, XRegs<T>::col(b, sub, k));
-        xr.convert(xv, act);
+        if (__syncthreads_or(xr.convert(xv, act))) {  // uniform over the workgroup
+            staged_exact<T, NORM>(args, nscale);
+            return;
+        }
     }
 
     // 4. pipelined walk over row groups
@@ -871,18 +995,23 @@ template <int T, int R, bool SX, int NW, bool NORM = false, bool DYN = false>
 hipError_t launch_staged_nw(const StagedArgs &sa, int nblk, int ngroups, hipStream_t s) {
     using F = Fmt<T>;
     const void *kern = reinterpret_cast<const void *>(&gemv_staged<T, R, SX, NW, NORM, DYN>);
-    static bool attr_set =  // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950)
-        hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
-    (void)attr_set;
-    const size_t lds = (SX ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)NW * R * F::CH * 16 +
-                       kRing * NW * R * 4 + 2 * kRing * NW * 4 + 16;
-    if (lds > 160 * 1024) return hipErrorNotSupported;
+    // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950).  The
+    // call has been refused for some instantiations: its error is cleared here, so
+    // that the launch's own status is the one reported, and such a kernel keeps 64 KB.
+    static const size_t lds_max = [kern] {
+        const bool ok = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+        (void)hipGetLastError();
+        return ok ? size_t(160) * 1024 : size_t(64) * 1024;
+    }();
+    // walk, claim counter, per-wave flags
+    const size_t base = staged_front(SX, nblk, NW, R, F::CH) + 4 + 4 * NW;
+    if (base > lds_max) return hipErrorNotSupported;
     const int slots = NW / sa.gw;
     const int need = (ngroups + slots - 1) / slots;
     // persistent grid: as many workgroups as fit at once (DYN: one per CU), capped by the work
-    int wgs = DYN ? cu_count() : resident_workgroups(kern, 64 * NW, lds);
+    int wgs = DYN ? cu_count() : resident_workgroups(kern, 64 * NW, base);
     if (wgs > need) wgs = need;
-    gemv_staged<T, R, SX, NW, NORM, DYN><<<wgs, 64 * NW, lds, s>>>(sa);
+    gemv_staged<T, R, SX, NW, NORM, DYN><<<wgs, 64 * NW, base, s>>>(sa);
     return hipGetLastError();
 }
 

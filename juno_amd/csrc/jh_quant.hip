@@ -1,15 +1,13 @@
 // jh_quant.hip -- dequantization (bit-exact) and quantization kernels.
 //
 // Dequantization restates LlamaTransformerHandler.dequantize
-// (LlamaTransformerHandler.java:873-1135).  Every product there is exact in
-// fp32 (an 11-bit fp16 significand times a 6- or 8-bit scale times a 4-, 6- or
-// 8-bit quant), so only the Q4_K "- min" rounds; the explicit _rn intrinsics
-// keep each step a separately rounded IEEE operation anyway.
+// (LlamaTransformerHandler.java:873-1135), unit by unit (jh_dequant.hpp).
 //
 // Quantization restates LoraMerge.requantize (LoraMerge.java:226-469) so that
 // benchmark and test inputs are the reference quantizer's bytes, produced on
 // the device.  One thread per block: the reference is sequential per block and
 // its rounding (Math.round, fp32 divisions) is reproduced exactly.
+#include "jh_dequant.hpp"
 #include "jh_device.hpp"
 #include "jh_kernels.hpp"
 
@@ -17,125 +15,8 @@ namespace jh {
 
 // ---------------------------------------------------------------- dequant
 
-// Each dequant_* function expands one unit (a 32- or 16-element sub-block, a
-// Q8_0 block or one F32 element) t of the packed image W into out.
-__device__ __forceinline__ void dequant_q4k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
-    const int64_t blk = t >> 3;
-    const int j = (int)(t & 7), g = j >> 1;
-    const uint8_t *bp = W + blk * 144;
-    const float d = half_bits_to_float(bp[0] | (bp[1] << 8));
-    const float dmin = half_bits_to_float(bp[2] | (bp[3] << 8));
-    const uint32_t s0 = bp[4] | (bp[5] << 8) | (bp[6] << 16) | ((uint32_t)bp[7] << 24);
-    const uint32_t s1 = bp[8] | (bp[9] << 8) | (bp[10] << 16) | ((uint32_t)bp[11] << 24);
-    const uint32_t s2 = bp[12] | (bp[13] << 8) | (bp[14] << 16) | ((uint32_t)bp[15] << 24);
-    int ls, lm;
-    q4k_scale_min(s0, s1, s2, j, ls, lm);
-    const float scale = __fmul_rn(d, (float)ls), mn = __fmul_rn(dmin, (float)lm);
-    const uint8_t *qs = bp + 16 + g * 32;
-    const int shift = (j & 1) * 4;
-    float *o = out + t * 32;
-    for (int i = 0; i < 32; i++) o[i] = __fsub_rn(__fmul_rn(scale, (float)((qs[i] >> shift) & 0x0F)), mn);
-}
-
-// dequantizeQ5K (LlamaTransformerHandler.java:1052-1093): the Q4_K layout plus a
-// 5th bit per element in qh (bit j of qh[l] for sub-block j).
-__device__ __forceinline__ void dequant_q5k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
-    const int64_t blk = t >> 3;
-    const int j = (int)(t & 7), g = j >> 1;
-    const uint8_t *bp = W + blk * 176;
-    const float d = half_bits_to_float(bp[0] | (bp[1] << 8));
-    const float dmin = half_bits_to_float(bp[2] | (bp[3] << 8));
-    const uint32_t s0 = bp[4] | (bp[5] << 8) | (bp[6] << 16) | ((uint32_t)bp[7] << 24);
-    const uint32_t s1 = bp[8] | (bp[9] << 8) | (bp[10] << 16) | ((uint32_t)bp[11] << 24);
-    const uint32_t s2 = bp[12] | (bp[13] << 8) | (bp[14] << 16) | ((uint32_t)bp[15] << 24);
-    int ls, lm;
-    q4k_scale_min(s0, s1, s2, j, ls, lm);
-    const float scale = __fmul_rn(d, (float)ls), mn = __fmul_rn(dmin, (float)lm);
-    const uint8_t *qh = bp + 16, *qs = bp + 48 + g * 32;
-    const int shift = (j & 1) * 4;
-    float *o = out + t * 32;
-    for (int i = 0; i < 32; i++) {
-        const int q = ((qs[i] >> shift) & 0x0F) | (((qh[i] >> j) & 1) << 4);
-        o[i] = __fsub_rn(__fmul_rn(scale, (float)q), mn);
-    }
-}
-
-__device__ __forceinline__ void dequant_q6k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
-    const int64_t blk = t >> 4;
-    const int s = (int)(t & 15), half = s >> 3, k = (s & 7) >> 1, is = s & 1;
-    const uint8_t *bp = W + blk * 210;
-    const float d = half_bits_to_float(bp[208] | (bp[209] << 8));
-    const float dk = __fmul_rn(d, (float)(int8_t)bp[192 + half * 8 + is + 2 * k]);
-    const uint8_t *ql = bp + half * 64 + ((k & 1) ? 32 : 0);
-    const uint8_t *qh = bp + 128 + half * 32;
-    const int nsh = (k >> 1) * 4, hsh = 2 * k;
-    float *o = out + blk * 256 + half * 128 + k * 32 + is * 16;
-    for (int i = 0; i < 16; i++) {
-        const int l = is * 16 + i;
-        const int q = (((ql[l] >> nsh) & 0x0F) | (((qh[l] >> hsh) & 3) << 4)) - 32;
-        o[i] = __fmul_rn(dk, (float)q);
-    }
-}
-
-__device__ __forceinline__ void dequant_q8_0(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
-    const uint8_t *bp = W + t * 34;
-    const float d = half_bits_to_float(bp[0] | (bp[1] << 8));
-    float *o = out + t * 32;
-    for (int i = 0; i < 32; i++) o[i] = __fmul_rn(d, (float)(int8_t)bp[2 + i]);
-}
-
-// dequantizeQ2K (LlamaTransformerHandler.java:915-952): unit t = 16 elements
-// of block t/16, half h = (t/8)&1, group k = t&7: elements h*128 + 16k + l take
-// the 2 bits at shift 2(k/2) of qs[32h + 16(k&1) + l] and scale byte sc[8h + k];
-// w = (d*(sc&15))*q - dmin*(sc>>4).
-__device__ __forceinline__ void dequant_q2k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
-    const int64_t blk = t >> 4;
-    const int h = (int)(t >> 3) & 1, k = (int)t & 7;
-    const uint8_t *bp = W + blk * 84;
-    const float d = half_bits_to_float(bp[80] | (bp[81] << 8)), dmin = half_bits_to_float(bp[82] | (bp[83] << 8));
-    const int sc = bp[8 * h + k];
-    const float dl = __fmul_rn(d, (float)(sc & 15)), ml = __fmul_rn(dmin, (float)(sc >> 4));
-    const uint8_t *qs = bp + 16 + 32 * h + 16 * (k & 1);
-    const int shift = 2 * (k >> 1);
-    float *o = out + blk * 256 + h * 128 + 16 * k;
-    for (int l = 0; l < 16; l++) o[l] = __fsub_rn(__fmul_rn(dl, (float)((qs[l] >> shift) & 3)), ml);
-}
-
-// dequantizeQ3K (LlamaTransformerHandler.java:954-1015): unit t = 16 elements
-// of block t/16, group is = t&15 = 8h + 2j + r: elements h*128 + 32j + 16r + l
-// take the 2 bits at shift 2j of qs[32h + 16r + l] and bit 4h + j of
-// hmask[16r + l]; w = (d*sc[is]) * ((low2 | hi<<2) - 4), exact.
-__device__ __forceinline__ void dequant_q3k(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
-    const int64_t blk = t >> 4;
-    const int is = (int)t & 15, h = is >> 3, j = (is >> 1) & 3, r = is & 1;
-    const uint8_t *bp = W + blk * 110;
-    const float d = half_bits_to_float(bp[108] | (bp[109] << 8));
-    // scale is: 4 low bits from byte is&7 (high nibble for is >= 8), 2 high bits
-    // from byte 8 + (is&3) at bit 2*(is/4) (the utmp words of :969-985)
-    const int lo4 = (bp[96 + (is & 7)] >> (is >= 8 ? 4 : 0)) & 15;
-    const int hi2 = (bp[104 + (is & 3)] >> (2 * (is >> 2))) & 3;
-    const float dl = __fmul_rn(d, (float)((lo4 | (hi2 << 4)) - 32));
-    const uint8_t *qs = bp + 32 + 32 * h + 16 * r, *hm = bp + 16 * r;
-    const int m = 1 << (4 * h + j);
-    float *o = out + blk * 256 + h * 128 + 32 * j + 16 * r;
-    for (int l = 0; l < 16; l++) {
-        const int q = (((qs[l] >> (2 * j)) & 3) | ((hm[l] & m) ? 4 : 0)) - 4;
-        o[l] = __fmul_rn(dl, (float)q);
-    }
-}
-
-__device__ __forceinline__ void dequant_f32(const uint8_t *__restrict__ W, int64_t t, float *__restrict__ out) {
-    out[t] = reinterpret_cast<const float *>(W)[t];
-}
-
 template <int T> __device__ __forceinline__ void dequant_unit(const uint8_t *W, int64_t t, float *out) {
-    if constexpr (T == 12) dequant_q4k(W, t, out);
-    else if constexpr (T == 13) dequant_q5k(W, t, out);
-    else if constexpr (T == 14) dequant_q6k(W, t, out);
-    else if constexpr (T == 8) dequant_q8_0(W, t, out);
-    else if constexpr (T == 10) dequant_q2k(W, t, out);
-    else if constexpr (T == 11) dequant_q3k(W, t, out);
-    else dequant_f32(W, t, out);
+    deq_unit<T>(W, t, [out](int64_t i, float v) { out[i] = v; });
 }
 
 template <int T> __global__ void dequant_k(const uint8_t *__restrict__ W, int64_t units, float *__restrict__ out) {

@@ -19,17 +19,12 @@ Three cases:
   * extreme_in_subblock: the same x, with only the large element's own weight
     zero, so the small elements of its sub-block (which share its x scale on
     the staged path) carry their part of the dot product.
-Bar: max rel-err 1e-3 with eps_r = 1e-3 * sum_c |w_rc x_c| (the GEMV bar); the
-plain relative error (no eps floor) is printed and must also stay within 1e-3
-on rows whose |y| is at least 1e-2 of sum_c |w_rc x_c|.
-
-One case is held to a different, stated bound: extreme_in_subblock on the
-B = 1 staged kernel.  Its x is rounded to 2^-31 of the largest |x| of each
-quant sub-block (exact for elements within 2^6 of it), so an element 1e-6 of
-its sub-block's outlier keeps only ~2^-11 of itself; the test asserts the
-kernel's error bound, sum_c |w_rc| * 2^-31 * max_g(c) |x| plus the fp32
-summation allowance, and prints the rel-err for the record.  The batched
-(fp16 hi + lo limb) kernels meet the 1e-3 bar there too.
+Bar, for every case and path: max rel-err 1e-3 with eps_r = 1e-3 * sum_c
+|w_rc x_c| (the GEMV bar); the plain relative error (no eps floor) must also
+stay within 1e-3 on rows whose |y| is at least 1e-2 of sum_c |w_rc x_c|.  On
+the B = 1 staged kernel extreme_in_subblock is the case its exact path
+exists for (an element 1e-6 of its sub-block's outlier would keep
+only ~2^-11 of itself in the 30-bit integer x alone).
 """
 import ctypes
 
@@ -85,19 +80,6 @@ def weights_zero_at(qtype, rows, cols, big, seed, whole_subblock=True):
     return w.reshape(-1)
 
 
-def staged_bound_ratio(qtype, deq, X, Y, ref_rows):
-    """max over rows of |y - ref| / (sum_c |w_rc| 2^-31 max_g(c)|x| + 1e-6 sum_c |w_rc x_c|):
-    the staged kernel's x rounding bound plus an fp32 summation allowance."""
-    G = 16 if qtype == O.Q6_K else 32
-    worst = 0.0
-    for j, ref in enumerate(ref_rows):
-        x = X[j].astype(np.float64)
-        gmax = np.repeat(np.abs(x).reshape(-1, G).max(axis=1), G)
-        bound = np.abs(deq) @ (gmax * 2.0 ** -31) + 1e-6 * (np.abs(deq) @ np.abs(x))
-        worst = max(worst, float((np.abs(Y[j].astype(np.float64) - ref) / bound).max()))
-    return worst
-
-
 def measure(qtype, raw, rows, cols, X, Y, label):
     deq = O.dequantize(qtype, raw, rows, cols).astype(np.float64)
     assert np.all(deq.reshape(rows, cols)[:, [c for c in range(cols) if abs(X[0, c]) >= 1e3]] == 0.0)
@@ -143,11 +125,6 @@ def test_wide_dynamic_range_x(be, kind, qtype, rows, cols, B):
     with be.upload_quant(mv.QuantizedTensor("w", qtype, rows * cols, raw.tobytes()), rows, cols) as dev:
         say(f"numerics {kind} type {qtype} {rows}x{cols} B={B}")
         Y = run(dev, X, rows)
-    worst, worst_plain, deq, refs = measure(qtype, raw, rows, cols, X, Y, f"{kind} type {qtype} {rows}x{cols} B={B}")
-    if kind == "extreme_in_subblock" and B == 1:
-        ratio = staged_bound_ratio(qtype, deq, X, Y, refs)
-        say(f"  staged kernel: max error / stated bound = {ratio:.3f}")
-        assert ratio <= 1.0
-        return
+    worst, worst_plain, _, _ = measure(qtype, raw, rows, cols, X, Y, f"{kind} type {qtype} {rows}x{cols} B={B}")
     assert worst <= TOL
     assert worst_plain <= TOL
