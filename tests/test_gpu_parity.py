@@ -275,12 +275,13 @@ MFMA_SHAPES = [
 
 @pytest.mark.parametrize("qtype,rows,cols", MFMA_SHAPES)
 def test_batched_mfma_8b_shapes(be, qtype, rows, cols):
-    """The MFMA path at the 8B / Phi-3 shapes, B in {16, 32, 64}, against the
-    oracle per column (weights with 1 % outliers at 10x, x with spikes)."""
+    """The batched path at the 8B / Phi-3 shapes, B in {8, 16, 32, 64} (config 4's
+    batches: B = 8 takes the MFMA kernel too), against the oracle per column
+    (weights with 1 % outliers at 10x, x with spikes)."""
     raw = O.quantize(qtype, weights(rows * cols, 400 + rows + qtype, outliers=True))
     deq = O.dequantize(qtype, raw, rows, cols)
     with upload(be, qtype, raw, rows, cols) as dev:
-        for B in (16, 32, 64):
+        for B in (8, 16, 32, 64):
             say("mfma", qtype, rows, cols, B)
             X = vec(cols, 500 + B, batch=B)
             X[:, ::131] *= 30.0
