@@ -200,6 +200,12 @@ int jh_rmsnorm_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const 
 int jh_rmsnorm_qmatvec_dev(const jh_qmat *m, const float *d_x, const float *d_res, const float *d_norm_w, float eps,
                            float *d_x_out, float *d_xn, float *d_y, void *stream);
 
+/* Device-side waits that gave up since the last call on this device (a
+ * column-tile ring cell of the staged kernel past its spin bound: that launch's
+ * results are then wrong); the count is cleared.  No counterpart in the
+ * reference (its matVecs have no cross-wave waits): for tests and health checks. */
+int jh_sync_faults(int device, unsigned int *count);
+
 /* The attention input norm fused into the grouped GEMV of the matrices that
  * read it: h = x + res, x_out = h (when not NULL; it must not alias x or res),
  * y_i = W_i rmsNorm(h, norm_w, eps) for n <= 8 matrices of one column count

@@ -699,6 +699,15 @@ int jh_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d
     return ok();
 }
 
+int jh_sync_faults(int device, unsigned int *count) {
+    if (!count) return fail(JH_EINVAL, "count must not be null");
+    int rc;
+    if ((rc = set_device(device))) return rc;
+    const hipError_t e = jh::sync_faults(count);
+    if (e != hipSuccess) return hip_fail("sync_faults", e);
+    return ok();
+}
+
 static int check_norm_args(const float *d_x, const float *d_res, const float *d_norm_w, const float *d_x_out,
                            const float *d_xn, int n) {
     if (!d_x || !d_norm_w || !d_xn) return fail(JH_EINVAL, "x, norm weights and xn scratch must not be null");

@@ -215,6 +215,9 @@ struct XImage {
 // partials][ring arrival / release counters]; then the claim counter and the
 // per-wave residual flags.
 constexpr int kRing = 4;  // cells per slot of the column-tile ring (a power of two)
+// Bounded device-side waits that gave up (the ring's cell waits): counted
+// here, read and cleared by sync_faults (jh_sync_faults).
+__device__ unsigned int g_sync_faults;
 __host__ __device__ constexpr size_t staged_front(bool sx, int nblk, int nw, int r, int ch) {
     return (sx ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)nw * r * ch * 16 +
            (size_t)kRing * nw * r * 4 + 2 * kRing * nw * 4;
@@ -850,8 +853,12 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
             const int cell = slot * kRing + (it & (kRing - 1));
             const int use = it / kRing;
             if (use > 0)
-                for (int spin = 0; spin < (1 << 22); spin++) {
+                for (int spin = 0;; spin++) {
                     if (__hip_atomic_load(ring_done + cell, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= use) break;
+                    if (spin == (1 << 22)) {  // never expected: counted (the sums are then wrong) rather than a hang
+                        if (lane == 0) __hip_atomic_fetch_add(&g_sync_faults, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
                     __builtin_amdgcn_s_sleep(1);
                 }
             float *pc = part + cell * gw * R;
@@ -1226,6 +1233,16 @@ hipError_t launch_gemv_staged_group(int n, const GroupProblem *p, hipStream_t s)
     sa.x = p[0].x;
     if (total == 0) return hipSuccess;
     return launch_staged_any(sa, p[0].type, s);
+}
+
+hipError_t sync_faults(unsigned *count) {
+    unsigned v = 0;
+    hipError_t e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_sync_faults), sizeof(v));
+    if (e != hipSuccess) return e;
+    const unsigned zero = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(g_sync_faults), &zero, sizeof(zero));
+    *count = v;
+    return e;
 }
 
 }  // namespace jh

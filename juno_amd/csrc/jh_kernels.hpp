@@ -69,6 +69,10 @@ struct NormSpec {
 hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, float *out, hipStream_t s,
                               const NormSpec *norm = nullptr);
 
+// Bounded device-side waits that gave up (the staged kernel's column-tile ring
+// cells) since the last call, on the current device; the count is cleared.
+hipError_t sync_faults(unsigned *count);
+
 // B = 1 coalesced, pipelined, int8-x kernel (jh_gemv_staged.hip); returns
 // hipErrorNotSupported for shapes it does not cover.
 bool staged_supported(int type, int cols);

@@ -75,6 +75,11 @@ for qtype, cols, rows_list in [(O.Q4_K, 4096, [333, 1000, 77]), (O.Q5_K, 3072, [
         print("group", qtype, rows, cols, f"{rel.max():.2e}", flush=True)
         assert rel.max() <= 1e-3, (qtype, rows, cols, rel.max())
         m.close()
+# no column-tile ring wait gave up (jh_sync_faults counts them)
+import ctypes
+from juno_amd import _lib
+nf = ctypes.c_uint(7)
+assert _lib.load().jh_sync_faults(0, ctypes.byref(nf)) == 0 and nf.value == 0, nf.value
 print("staged-ok", worst)
 '''
 
