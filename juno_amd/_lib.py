@@ -98,8 +98,22 @@ def load() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
+        check_fresh(L)
         _lib = L
     return _lib
+
+
+def check_fresh(L) -> None:
+    """Refuse a library built from other sources than the tree's (jh_version
+    carries the hash build.py computed over csrc/ and include/).
+    JUNO_ALLOW_STALE_LIB=1 skips the check (A/B runs of saved builds)."""
+    from . import build as _build
+    got = L.jh_version().decode()
+    want = _build.source_hash()
+    if os.environ.get("JUNO_ALLOW_STALE_LIB") == "1" or got.endswith("src:" + want):
+        return
+    raise ImportError(f"{LIB_PATH} is stale ({got}); the sources hash to {want}: "
+                      "rebuild with `python -m juno_amd.build`")
 
 
 def last_error() -> str:

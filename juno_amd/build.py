@@ -7,6 +7,7 @@ the compiler from emitting packed-fp32 VALU instructions.
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import subprocess
 import sys
@@ -20,8 +21,28 @@ FLAGS = [*os.environ.get("JH_EXTRA_FLAGS", "").split(), "--offload-arch=gfx950",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+
+
+def source_hash() -> str:
+    """SHA-256 (first 16 hex digits) over the library's sources: every file in
+    csrc/ and include/ by name and content, plus the compile flags.  Built into
+    the library (jh_version) and checked by _lib.load(), so that a libjunohip.so
+    left from other sources is refused rather than run."""
+    h = hashlib.sha256()
+    for d in (CSRC, INCLUDE):
+        for name in sorted(os.listdir(d)):
+            if name.endswith((".hip", ".cpp", ".hpp", ".h")):
+                h.update(name.encode() + b"\0")
+                with open(os.path.join(d, name), "rb") as f:
+                    h.update(f.read() + b"\0")
+    h.update(" ".join(FLAGS).encode())
+    return h.hexdigest()[:16]
+
+
 def build(verbose: bool = False) -> str:
-    cmd = [HIPCC, *FLAGS, *[os.path.join(CSRC, s) for s in SOURCES], "-o", OUT + ".tmp"]
+    cmd = [HIPCC, *FLAGS, f'-DJH_SRC_HASH="{source_hash()}"', *[os.path.join(CSRC, s) for s in SOURCES],
+           "-o", OUT + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -356,7 +356,12 @@ int jh_internal_fail(int code, const char *msg) {
     return fail(code, "%s", msg);
 }
 
-const char *jh_version(void) { return "junohip 0.1 gfx950"; }
+#ifndef JH_SRC_HASH
+#define JH_SRC_HASH "unknown"
+#endif
+// The build (juno_amd/build.py) passes the hash of the sources it compiled, so a
+// loader can refuse a library left from other sources.
+const char *jh_version(void) { return "junohip 0.1 gfx950 src:" JH_SRC_HASH; }
 
 int jh_device_count(int *count) {
     if (!count) return fail(JH_EINVAL, "count must not be null");

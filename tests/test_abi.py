@@ -46,6 +46,25 @@ def test_version_and_last_error_without_gpu():
     assert isinstance(L.jh_last_error(), bytes)
 
 
+def test_library_matches_its_sources(monkeypatch):
+    """The loaded library carries the hash of the sources it was built from, and
+    a library from other sources is refused (unless JUNO_ALLOW_STALE_LIB=1)."""
+    from juno_amd import build
+    L = _lib.load()
+    assert L.jh_version().decode().endswith("src:" + build.source_hash())
+
+    class Old:
+        @staticmethod
+        def jh_version():
+            return b"junohip 0.1 gfx950 src:0000000000000000"
+
+    monkeypatch.delenv("JUNO_ALLOW_STALE_LIB", raising=False)
+    with pytest.raises(ImportError, match="stale"):
+        _lib.check_fresh(Old)
+    monkeypatch.setenv("JUNO_ALLOW_STALE_LIB", "1")
+    _lib.check_fresh(Old)
+
+
 def test_raw_byte_count_matches_reference_formula():
     L = _lib.load()
     out = ctypes.c_int64()
