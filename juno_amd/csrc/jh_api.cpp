@@ -422,7 +422,9 @@ int jh_raw_byte_count(int type, int64_t nelems, int64_t *out) {
     int qk, bb;
     if (!type_geometry(type, &qk, &bb)) return fail(JH_EUNSUPPORTED, "No byte-size formula for GGML type %d", type);
     if (!out) return fail(JH_EINVAL, "out must not be null");
-    *out = (nelems / qk) * bb;
+    // Java long arithmetic: the product wraps (two's complement) instead of
+    // being undefined as a signed overflow in C++
+    *out = (int64_t)((uint64_t)(nelems / qk) * (uint64_t)bb);
     return ok();
 }
 

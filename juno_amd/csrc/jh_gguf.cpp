@@ -91,13 +91,19 @@ struct jh_gguf {
 
 namespace {
 
+// Java long arithmetic (the reference's offsets and sizes are longs): products
+// and sums wrap in two's complement instead of overflowing (undefined in C++);
+// a wrapped value then fails the reads' bounds checks.
+inline int64_t wmul(int64_t a, int64_t b) { return (int64_t)((uint64_t)a * (uint64_t)b); }
+inline int64_t wadd(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+
 // ------------------------------------------------------------------ positional reads
 struct Reader {
     int fd;
     int64_t size;
     bool ok = true;
     bool read(int64_t pos, void *dst, size_t n) {
-        if (!ok || pos < 0 || pos + (int64_t)n > size) return ok = false;
+        if (!ok || pos < 0 || pos > size || n > (uint64_t)(size - pos)) return ok = false;
         uint8_t *p = static_cast<uint8_t *>(dst);
         while (n) {
             const ssize_t r = pread(fd, p, n, pos);
@@ -280,16 +286,16 @@ constexpr int64_t kAlign = 32;
 
 bool raw_bytes(int type, int64_t nelems, int64_t *out) {  // rawByteCount (:347-360)
     switch (type) {
-    case 0: *out = nelems * 4; return true;
+    case 0: *out = wmul(nelems, 4); return true;
     case 1:
-    case 30: *out = nelems * 2; return true;
-    case 8: *out = nelems / 32 * 34; return true;
-    case 2: *out = nelems / 32 * 18; return true;
-    case 10: *out = nelems / 256 * 84; return true;
-    case 11: *out = nelems / 256 * 110; return true;
-    case 12: *out = nelems / 256 * 144; return true;
-    case 13: *out = nelems / 256 * 176; return true;
-    case 14: *out = nelems / 256 * 210; return true;
+    case 30: *out = wmul(nelems, 2); return true;
+    case 8: *out = wmul(nelems / 32, 34); return true;
+    case 2: *out = wmul(nelems / 32, 18); return true;
+    case 10: *out = wmul(nelems / 256, 84); return true;
+    case 11: *out = wmul(nelems / 256, 110); return true;
+    case 12: *out = wmul(nelems / 256, 144); return true;
+    case 13: *out = wmul(nelems / 256, 176); return true;
+    case 14: *out = wmul(nelems / 256, 210); return true;
     default: return false;
     }
 }
@@ -371,7 +377,7 @@ int jh_gguf_open(const char *path, jh_gguf **out) {
         for (int d = 0; d < nd; d++) {
             const int64_t v = (int64_t)rd.get<uint64_t>(pos);
             t.dims.push_back(v);
-            t.nelems *= v;
+            t.nelems = wmul(t.nelems, v);  // :162-164
         }
         t.type = (int32_t)rd.get<uint32_t>(pos);
         t.offset = (int64_t)rd.get<uint64_t>(pos);
@@ -475,7 +481,7 @@ int jh_gguf_tensor_info(const jh_gguf *g, int64_t index, const char **name, int 
     if (dims)
         for (size_t d = 0; d < t.dims.size(); d++) dims[d] = t.dims[d];
     if (nelems) *nelems = t.nelems;
-    if (abs_offset) *abs_offset = g->data_offset + t.offset;
+    if (abs_offset) *abs_offset = wadd(g->data_offset, t.offset);
     return JH_OK;
 }
 
@@ -491,9 +497,9 @@ int jh_gguf_tensor_read(const jh_gguf *g, int64_t index, void *dst, size_t cap, 
     if (!dst) return JH_OK;  // size query
     if ((size_t)n > cap) return gfail(JH_EINVAL, "buffer of %zu bytes is smaller than the tensor (%lld bytes)", cap, (long long)n);
     Reader rd{g->fd, g->file_size};
-    if (!rd.read(g->data_offset + t.offset, dst, (size_t)n))
+    if (n < 0 || !rd.read(wadd(g->data_offset, t.offset), dst, (size_t)n))
         return gfail(JH_EIO, "Expected %lld bytes of %s at offset %lld", (long long)n, t.name.c_str(),
-                     (long long)(g->data_offset + t.offset));
+                     (long long)wadd(g->data_offset, t.offset));
     return JH_OK;
 }
 
@@ -509,6 +515,9 @@ int jh_gguf_stream_to_device(const jh_gguf *g, int64_t index, uint8_t *d_dst, in
     const TensorInfo &t = g->tensors[(size_t)index];
     int64_t n = 0;
     if (!raw_bytes(t.type, t.nelems, &n)) return gfail(JH_EUNSUPPORTED, "No byte-size formula for GGML type %d", t.type);
+    if (n < 0 || t.nelems < 0 || (!t.dims.empty() && t.dims[0] <= 0))
+        return gfail(JH_EFORMAT, "tensor %s: bad shape (nelems %lld, dims[0] %lld)", t.name.c_str(),
+                     (long long)t.nelems, (long long)(t.dims.empty() ? 1 : t.dims[0]));
     if (nbytes_out) *nbytes_out = n;
     if (type_out) *type_out = t.type;
     if (cols_out) *cols_out = t.dims.empty() ? 1 : t.dims[0];
@@ -534,9 +543,9 @@ int jh_gguf_stream_to_device(const jh_gguf *g, int64_t index, uint8_t *d_dst, in
             rc = gfail(JH_EHIP, "hipEventSynchronize failed");
             break;
         }
-        if (!rd.read(g->data_offset + t.offset + at, stage[k], len)) {
+        if (!rd.read(wadd(wadd(g->data_offset, t.offset), at), stage[k], len)) {
             rc = gfail(JH_EIO, "Expected %lld bytes of %s at offset %lld", (long long)n, t.name.c_str(),
-                       (long long)(g->data_offset + t.offset));
+                       (long long)wadd(g->data_offset, t.offset));
             break;
         }
         if (hipMemcpyAsync(d_dst + at, stage[k], len, hipMemcpyHostToDevice, s) != hipSuccess ||
