@@ -11,6 +11,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <dlfcn.h>
+
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -519,7 +521,73 @@ int jh_qmat_info(const jh_qmat *m, int *type, int *rows, int *cols, size_t *nbyt
     return ok();
 }
 
+// ------------------------------------------------------------------ juno.MatVec ranges
+// The reference wraps every matVec in a JFR event "juno.MatVec" with the backend
+// label, rows and cols (MatVecEvent.java:46-72, MatVecBackend.java:36-64).  Here
+// the same call sites push a roctx range "juno.MatVec backend=<label> rows=R
+// cols=C batch=B" when JUNO_ROCTX=1 (rocprofv3 --marker-trace records them);
+// the roctx library is opened at the first such call, so the library has no
+// link-time dependency on it.  The range covers the host call: for the synchronous entry
+// points that is the H2D copy, the kernels and the D2H copy, as the reference's
+// event covers its transfers; for the _dev entry points it is the enqueue.
+namespace {
+typedef int (*roctx_push_t)(const char *);
+typedef int (*roctx_pop_t)();
+struct Roctx {
+    roctx_push_t push = nullptr;
+    roctx_pop_t pop = nullptr;
+};
+const Roctx &roctx() {
+    static const Roctx r = [] {
+        Roctx t;
+        const char *e = getenv("JUNO_ROCTX");
+        if (!e || strcmp(e, "1") != 0) return t;
+        // rocprofv3 intercepts the rocprofiler-sdk roctx library; the older
+        // roctracer one (libroctx64) serves roctracer-based tools
+        void *h = nullptr;
+        for (const char *lib : {"librocprofiler-sdk-roctx.so.1", "/opt/rocm/lib/librocprofiler-sdk-roctx.so.1",
+                                "libroctx64.so", "/opt/rocm/lib/libroctx64.so"})
+            if (!h) h = dlopen(lib, RTLD_NOW | RTLD_LOCAL);
+        if (!h) return t;
+        t.push = reinterpret_cast<roctx_push_t>(dlsym(h, "roctxRangePushA"));
+        t.pop = reinterpret_cast<roctx_pop_t>(dlsym(h, "roctxRangePop"));
+        if (!t.push || !t.pop) t.push = nullptr, t.pop = nullptr;
+        return t;
+    }();
+    return r;
+}
+// MatVecBackend labels of the resident quantized matrices (juno_amd/matvec.py MatVecBackend.for_type)
+const char *backend_label(int type) {
+    switch (type) {
+    case JH_TYPE_F32: return "rocm-resident";
+    case 10: return "rocm-resident-q2k";
+    case 11: return "rocm-resident-q3k";
+    case 12: return "rocm-resident-q4k";
+    case 13: return "rocm-resident-q5k";
+    case 14: return "rocm-resident-q6k";
+    case 8: return "rocm-resident-q8_0";
+    default: return "rocm-resident";
+    }
+}
+struct MatVecRange {
+    bool on = false;
+    MatVecRange(const char *backend, long long rows, long long cols, int batch) {
+        const Roctx &r = roctx();
+        if (!r.push) return;
+        char msg[160];
+        snprintf(msg, sizeof msg, "juno.MatVec backend=%s rows=%lld cols=%lld batch=%d", backend, rows, cols, batch);
+        r.push(msg);
+        on = true;
+    }
+    ~MatVecRange() {
+        if (on) roctx().pop();
+    }
+};
+}  // namespace
+
 int jh_qmatvec_batched(jh_ctx *ctx, const jh_qmat *m, const float *X, int B, float *Y, int row_start, int row_end) {
+    const MatVecRange range(m ? backend_label(m->type) : "rocm-resident", (long long)row_end - row_start,
+                            m ? m->cols : 0, B);
     int rc;
     if (!ctx) return fail(JH_EINVAL, "ctx must not be null");
     if ((rc = check_qmat(m)) || (rc = check_range(m, row_start, row_end))) return rc;
@@ -588,6 +656,8 @@ int jh_qmatvec_dev(const jh_qmat *m, const float *d_x, float *d_y, int row_start
 
 int jh_qmatvec_batched_dev(const jh_qmat *m, const float *d_X, int B, float *d_Y, int row_start, int row_end,
                            void *stream) {
+    const MatVecRange range(m ? backend_label(m->type) : "rocm-resident", (long long)row_end - row_start,
+                            m ? m->cols : 0, B);
     int rc;
     if ((rc = check_qmat(m)) || (rc = check_range(m, row_start, row_end))) return rc;
     if (B < 0) return fail(JH_EINVAL, "B=%d must be >= 0", B);
@@ -633,6 +703,9 @@ int jh_qmatvec_group_dev(int n, const jh_qmat *const *mats, const float *const *
     if (n < 0 || n > jh::kMaxGroup) return fail(JH_EINVAL, "n=%d outside [0, %d]", n, jh::kMaxGroup);
     if (n == 0) return ok();
     if (!mats || !d_x || !d_y) return fail(JH_EINVAL, "mats, x and y must not be null");
+    long long grows = 0;
+    for (int i = 0; i < n; i++) grows += mats[i] ? mats[i]->rows : 0;
+    const MatVecRange range("rocm-resident-group", grows, mats[0] ? mats[0]->cols : 0, 1);
     jh::GroupProblem all[jh::kMaxGroup];
     int rc;
     for (int i = 0; i < n; i++) {
@@ -855,6 +928,9 @@ int jh_qmatvec_batched_group_dev(int n, const jh_qmat *const *mats, const float 
     if (B < 0) return fail(JH_EINVAL, "B=%d must be >= 0", B);
     if (n == 0 || B == 0) return ok();
     if (!mats || !d_X || !d_Y) return fail(JH_EINVAL, "mats, X and Y must not be null");
+    long long grows = 0;
+    for (int i = 0; i < n; i++) grows += mats[i] ? mats[i]->rows : 0;
+    const MatVecRange range("rocm-resident-group", grows, mats[0] ? mats[0]->cols : 0, B);
     int rc;
     jh::MfmaDesc d[jh::kMaxMfmaGroup];
     for (int i = 0; i < n; i++) {

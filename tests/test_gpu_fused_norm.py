@@ -35,6 +35,9 @@ def say(*a):
 
 def device_matrix(be, qtype, rows, cols, seed):
     import torch
+    if qtype in (O.Q2_K, O.Q3_K):  # no quantizer for these in the reference: random blocks, small d
+        from test_oracle_q2q3 import random_blocks
+        return be.upload_quant(qtype, rows, cols, random_blocks(qtype, rows, cols, seed))
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     w = torch.randn(rows * cols, generator=g, device="cuda").mul_(0.02)
@@ -144,6 +147,7 @@ def test_rmsnorm_output_projection(qt, rows, cols):
     (3072, [(O.Q8_0, 3072), (O.Q5_K, 768)]),
     (8192, [(O.Q4_K, 512), (O.Q8_0, 256)]),                     # the widest input the LDS image takes
     (14336, [(O.Q6_K, 300)]),                                    # wider: the unfused pair
+    (2048, [(O.Q2_K, 1024), (O.Q3_K, 512), (O.Q4_K, 256)]),      # the Q2_K / Q3_K bodies of the fused group kernel
 ])
 def test_rmsnorm_qkv_group(cols, shapes):
     """The attention norm fused into the one-shot grouped q / k / v launch
@@ -202,3 +206,31 @@ def test_rmsnorm_qkv_group(cols, shapes):
     finally:
         for m in mats:
             m.close()
+
+
+STATIC_CHILD = r'''
+import sys
+sys.path.insert(0, "tests")
+import test_gpu_fused_norm as T
+import oracle as O
+for qt, rows, cols in [(O.Q4_K, 14336, 4096)]:
+    T.test_rmsnorm_swiglu(qt, rows, cols)
+for qt, rows, cols in [(O.Q6_K, 32000, 2048)]:
+    T.test_rmsnorm_output_projection(qt, rows, cols)
+print("static-ok", flush=True)
+'''
+
+
+def test_fused_norm_static_layout():
+    """The SwiGLU and output-projection fusions through the static staged layout
+    (JUNO_STAGED_DYN=0: 4-wave workgroups with equal shares, the NW = 4 NORM
+    kernels), in a child process (the switch is read once per process)."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, JUNO_STAGED_DYN="0")
+    r = subprocess.run([sys.executable, "-u", "-c", STATIC_CHILD], env=env, cwd=root, capture_output=True,
+                       text=True, timeout=300)
+    print(r.stdout[-3000:])
+    assert r.returncode == 0 and "static-ok" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
