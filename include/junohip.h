@@ -246,6 +246,11 @@ int jh_qmatvec_batched_group_dev(int n, const jh_qmat *const *mats, const float 
  * unsplit, B <= 32: the output projection).  No counterpart in the reference;
  * for tests that must reach a given kernel. */
 int jh_qmatvec_batched_plan(int n, const jh_qmat *const *mats, int B, int *kernel, int *ksplit);
+/* The same plan for one matrix of a given format and shape, rows [row_start,
+ * row_end), without a device or a matrix (host-only arithmetic): for CPU
+ * checks of the kernels' address arithmetic. */
+int jh_qmatvec_batched_plan_shape(int ggml_type, int cols, int row_start, int row_end, int B, int *kernel,
+                                  int *ksplit);
 
 /* Diagnostics of the per-stream library workspace (see Conventions): the
  * scratch bytes the stream `stream` on `device` currently has (0 before its

@@ -40,6 +40,7 @@ SIGNATURES = {
     "jh_qmatvec_batched_noalloc_dev": (_I, [_P, _P, _I, _P, _I, _I, _P]),
     "jh_qmatvec_group_dev": (_I, [_I, _P, _P, _P, _P]),
     "jh_sync_faults": (_I, [_I, _P]),
+    "jh_qmatvec_batched_plan_shape": (_I, [_I, _I, _I, _I, _I, _P, _P]),
     "jh_qmatvec_batched_group_dev": (_I, [_I, _P, _P, _I, _P, _P]),
     "jh_qmatvec_swiglu_dev": (_I, [_P, _P, _P, _P, _P]),
     "jh_rmsnorm_qmatvec_swiglu_dev": (_I, [_P, _P, _P, _P, _P, ctypes.c_float, _P, _P, _P, _P]),

@@ -328,6 +328,22 @@ extern "C" {
 
 const char *jh_last_error(void) { return g_last_error.c_str(); }
 
+int jh_qmatvec_batched_plan_shape(int ggml_type, int cols, int row_start, int row_end, int B, int *kernel,
+                                  int *ksplit) {
+    if (!kernel || !ksplit) return fail(JH_EINVAL, "kernel and ksplit must not be null");
+    int qk, bb;
+    if (!type_geometry(ggml_type, &qk, &bb)) return fail(JH_EUNSUPPORTED, "no block geometry for GGML type %d", ggml_type);
+    if (cols <= 0 || cols % qk || row_start < 0 || row_end < row_start)
+        return fail(JH_EINVAL, "invalid shape: cols=%d rows [%d, %d)", cols, row_start, row_end);
+    // the planner reads formats, sizes and alignment only: a 256-byte-aligned stand-in address will do
+    const uint8_t *w = reinterpret_cast<const uint8_t *>(uintptr_t(1) << 20);
+    const jh::MfmaDesc d{ggml_type, w, (size_t)(cols / qk) * bb, cols, row_start, row_end,
+                         reinterpret_cast<const float *>(w), nullptr};
+    *ksplit = 1;
+    *kernel = B >= jh::kMfmaMinBatch ? jh::mfma_group_plan(1, &d, B, ksplit) : 0;
+    return ok();
+}
+
 int jh_qmatvec_batched_plan(int n, const jh_qmat *const *mats, int B, int *kernel, int *ksplit) {
     if (n < 1 || n > jh::kMaxMfmaGroup) return fail(JH_EINVAL, "n=%d outside [1, %d]", n, jh::kMaxMfmaGroup);
     if (!mats || !kernel || !ksplit) return fail(JH_EINVAL, "mats, kernel and ksplit must not be null");
