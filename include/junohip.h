@@ -206,6 +206,14 @@ int jh_rmsnorm_qmatvec_dev(const jh_qmat *m, const float *d_x, const float *d_re
  * reference (its matVecs have no cross-wave waits): for tests and health checks. */
 int jh_sync_faults(int device, unsigned int *count);
 
+/* Timeline builds only (compiled with -DJH_TIMELINE by juno_amd/timeline.py,
+ * never the shipped library; JH_EUNSUPPORTED otherwise): n entries of the
+ * staged B = 1 walk's per-wave s_memrealtime stamps (100 MHz) of the last
+ * launch, 4 per wave at (workgroup * 16 + wave) * 4: entry, after the x
+ * prologue, first row group landed, end of the walk.  No counterpart in the
+ * reference; a profiling aid. */
+int jh_debug_timeline(int device, uint64_t *out, size_t n);
+
 /* The attention input norm fused into the grouped GEMV of the matrices that
  * read it: h = x + res, x_out = h (when not NULL; it must not alias x or res),
  * y_i = W_i rmsNorm(h, norm_w, eps) for n <= 8 matrices of one column count

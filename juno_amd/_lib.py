@@ -10,7 +10,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libjunohip.so")
+# JUNO_LIB_PATH: another build of the library (juno_amd/timeline.py's instrumented variant)
+LIB_PATH = os.environ.get("JUNO_LIB_PATH", os.path.join(HERE, "libjunohip.so"))
 
 JH_OK, JH_EINVAL, JH_ENOMEM, JH_EHIP, JH_EUNSUPPORTED, JH_ECLOSED, JH_ENODEV, JH_EFORMAT, JH_EIO = range(9)
 
@@ -40,6 +41,7 @@ SIGNATURES = {
     "jh_qmatvec_batched_noalloc_dev": (_I, [_P, _P, _I, _P, _I, _I, _P]),
     "jh_qmatvec_group_dev": (_I, [_I, _P, _P, _P, _P]),
     "jh_sync_faults": (_I, [_I, _P]),
+    "jh_debug_timeline": (_I, [_I, _P, ctypes.c_size_t]),
     "jh_qmatvec_batched_plan_shape": (_I, [_I, _I, _I, _I, _I, _P, _P]),
     "jh_qmatvec_batched_group_dev": (_I, [_I, _P, _P, _I, _P, _P]),
     "jh_qmatvec_swiglu_dev": (_I, [_P, _P, _P, _P, _P]),

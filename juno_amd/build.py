@@ -14,7 +14,8 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
-OUT = os.path.join(HERE, "libjunohip.so")
+# JUNO_LIB_OUT: another output path (juno_amd/timeline.py builds its instrumented variant there)
+OUT = os.environ.get("JUNO_LIB_OUT", os.path.join(HERE, "libjunohip.so"))
 SOURCES = ["jh_api.cpp", "jh_gemv.hip", "jh_gemv_staged.hip", "jh_quant.hip", "jh_mfma.hip", "jh_decode.hip", "jh_gguf.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [*os.environ.get("JH_EXTRA_FLAGS", "").split(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared", "-Wall",

@@ -795,6 +795,16 @@ int jh_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d
     return ok();
 }
 
+int jh_debug_timeline(int device, uint64_t *out, size_t n) {
+    if (!out && n) return fail(JH_EINVAL, "out must not be null");
+    int rc;
+    if ((rc = set_device(device))) return rc;
+    const hipError_t e = jh::timeline_read(reinterpret_cast<unsigned long long *>(out), n);
+    if (e == hipErrorNotSupported) return fail(JH_EUNSUPPORTED, "not a timeline build (-DJH_TIMELINE)");
+    if (e != hipSuccess) return hip_fail("timeline read", e);
+    return ok();
+}
+
 int jh_sync_faults(int device, unsigned int *count) {
     if (!count) return fail(JH_EINVAL, "count must not be null");
     int rc;

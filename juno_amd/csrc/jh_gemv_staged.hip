@@ -218,6 +218,22 @@ constexpr int kRing = 4;  // cells per slot of the column-tile ring (a power of 
 // Bounded device-side waits that gave up (the ring's cell waits): counted
 // here, read and cleared by sync_faults (jh_sync_faults).
 __device__ unsigned int g_sync_faults;
+
+// Timeline builds (-DJH_TIMELINE, juno_amd/timeline.py; never the shipped
+// library): per wave of the DYN walk, s_memrealtime (100 MHz) at entry, after
+// the x prologue's barrier, once the first row group has landed, and at the end
+// of the walk; slot = (workgroup * 16 + wave) * 4, the last launch's values.
+#ifdef JH_TIMELINE
+constexpr int kTlWaves = 4096;
+__device__ unsigned long long g_timeline[kTlWaves * 4];
+#define JH_TL(k)                                                                                       \
+    do {                                                                                               \
+        if (DYN && (threadIdx.x & 63) == 0 && (int)blockIdx.x * NW + wave < kTlWaves)                  \
+            g_timeline[((int)blockIdx.x * NW + wave) * 4 + (k)] = __builtin_amdgcn_s_memrealtime();    \
+    } while (0)
+#else
+#define JH_TL(k) do {} while (0)
+#endif
 __host__ __device__ constexpr size_t staged_front(bool sx, int nblk, int nw, int r, int ch) {
     return (sx ? ((XImage::bytes(nblk) + 15) & ~size_t(15)) : 0) + (size_t)nw * r * ch * 16 +
            (size_t)kRing * nw * r * 4 + 2 * kRing * nw * 4;
@@ -633,6 +649,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     // wave-uniform values live in SGPRs: derive them from a readfirstlane'd wave id
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
+    JH_TL(0);
     const int nb = args.nb, nrows = args.nrows, gw = args.gw, tb = args.tb;
     const size_t pitch = args.pitch;
     constexpr bool shared_x = SX;  // gw == 1: every wave needs all of x
@@ -780,6 +797,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
         const bool wneed = __builtin_amdgcn_ballot_w64(need) != 0;  // over all lanes of the wave
         if (lane == 0) xneed[wave] = wneed;
         __syncthreads();
+        JH_TL(1);
         int anyneed = 0;
 #pragma unroll
         for (int w = 0; w < NW; w++) anyneed |= xneed[w];
@@ -802,6 +820,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     if (SX && gw != 1 && grp >= ngroups) return;  // fewer groups than slots: this slot has none
     park(buf0);
     wave_lds_sync();
+    JH_TL(2);
     int it = 0;
     while (true) {
         int cstart[R];
@@ -840,7 +859,10 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
                         if (r0 + i < nrows) store(r0 + i, s[i]);
                 }
             }
-            if (next >= ngroups) break;
+            if (next >= ngroups) {
+                JH_TL(3);
+                break;
+            }
         } else if constexpr (SX) {
             // Column tiles meet in a ring of kRing cells per slot instead of at a
             // workgroup barrier, so that a wave's arithmetic overlaps the other
@@ -1243,6 +1265,17 @@ hipError_t sync_faults(unsigned *count) {
     e = hipMemcpyToSymbol(HIP_SYMBOL(g_sync_faults), &zero, sizeof(zero));
     *count = v;
     return e;
+}
+
+hipError_t timeline_read(unsigned long long *out, size_t n) {
+#ifdef JH_TIMELINE
+    if (n > (size_t)kTlWaves * 4) n = (size_t)kTlWaves * 4;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_timeline), n * sizeof(unsigned long long));
+#else
+    (void)out;
+    (void)n;
+    return hipErrorNotSupported;
+#endif
 }
 
 }  // namespace jh

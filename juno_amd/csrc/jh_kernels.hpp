@@ -72,6 +72,8 @@ hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, 
 // Bounded device-side waits that gave up (the staged kernel's column-tile ring
 // cells) since the last call, on the current device; the count is cleared.
 hipError_t sync_faults(unsigned *count);
+// Timeline builds only (-DJH_TIMELINE): the staged walk's per-wave timestamps.
+hipError_t timeline_read(unsigned long long *out, size_t n);
 
 // B = 1 coalesced, pipelined, int8-x kernel (jh_gemv_staged.hip); returns
 // hipErrorNotSupported for shapes it does not cover.

@@ -1,0 +1,162 @@
+"""Per-wave timeline of the staged B = 1 walk (the dominant kernel: the grouped
+Q4_K [ffn_gate, ffn_up] launch at Llama-3-8B shapes, 2 x 14336 x 4096).
+
+Two steps, because the instrumented library is built on the CPU and run on the
+GPU box:
+
+    python -m juno_amd.timeline build    # juno_amd/_timeline/libjunohip.so, compiled with -DJH_TIMELINE
+    python -m juno_amd.timeline run      # the launches and the summary (markdown on stdout)
+
+The instrumented build stamps s_memrealtime (100 MHz) per wave of the DYN walk
+at entry, after the x prologue's barrier, once its first row group has landed
+in LDS, and at the end of its walk (jh_debug_timeline).  The shipped library
+has no stamps (jh_debug_timeline returns JH_EUNSUPPORTED there).  Each launch
+is timed relative to its earliest wave start; the summary gives medians and
+spreads over launches, with the weights of 8 distinct layers so that no launch
+finds its matrices in the 256 MB MALL.
+"""
+from __future__ import annotations
+
+import json
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+OUT_DIR = os.path.join(HERE, "_timeline")
+LIB = os.path.join(OUT_DIR, "libjunohip.so")
+FLAGS = "-DJH_TIMELINE"
+HIDDEN, FFN, LAYERS, REPS = 4096, 14336, 8, 4
+TICK_NS = 10.0  # s_memrealtime runs at 100 MHz
+
+
+def build() -> str:
+    os.makedirs(OUT_DIR, exist_ok=True)
+    env = dict(os.environ, JH_EXTRA_FLAGS=FLAGS, JUNO_LIB_OUT=LIB)
+    subprocess.run([sys.executable, "-m", "juno_amd.build"], env=env, check=True, cwd=os.path.dirname(HERE))
+    return LIB
+
+
+def _pct(a, q):
+    import numpy as np
+    return float(np.percentile(a, q))
+
+
+def run_child() -> dict:
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from juno_amd import _lib
+    from juno_amd import matvec as mv
+
+    L = _lib.load()
+    be = mv.GpuContext.shared(0).create_mat_vec()
+    s = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    mats = []
+    for _ in range(LAYERS):
+        pair = []
+        for _ in range(2):
+            w = torch.randn(FFN * HIDDEN, generator=g, device="cuda").mul_(0.02)
+            pair.append(be.quantize_dev(mv.Q4_K, w.data_ptr(), FFN, HIDDEN, s.cuda_stream))
+            del w
+        mats.append(pair)
+    torch.cuda.synchronize()
+    x = torch.randn(HIDDEN, generator=g, device="cuda")
+    ys = [torch.empty(FFN, device="cuda") for _ in range(2)]
+    V = ctypes.c_void_p
+    n_slots = 4096 * 4
+    buf = (ctypes.c_uint64 * n_slots)()
+    launches = []
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for rep in range(REPS + 1):
+        for pair in mats:
+            hs = (V * 2)(pair[0].handle, pair[1].handle)
+            xs = (V * 2)(x.data_ptr(), x.data_ptr())
+            yp = (V * 2)(ys[0].data_ptr(), ys[1].data_ptr())
+            ctypes.memset(buf, 0, ctypes.sizeof(buf))
+            e0.record(s)
+            if L.jh_qmatvec_group_dev(2, hs, xs, yp, V(s.cuda_stream)):
+                raise RuntimeError(_lib.last_error())
+            e1.record(s)
+            torch.cuda.synchronize()
+            if L.jh_debug_timeline(0, buf, n_slots):
+                raise RuntimeError(_lib.last_error())
+            if rep == 0:
+                continue  # warm-up pass
+            t = np.frombuffer(buf, dtype=np.uint64).reshape(-1, 4).astype(np.int64)
+            t = t[t[:, 0] > 0]
+            base = t[:, 0].min()
+            rel = (t - base) * TICK_NS / 1e3  # us
+            wg_end = rel[:, 3].reshape(-1, 16).max(axis=1)
+            launches.append({
+                "waves": int(len(rel)),
+                "event_us": float(e0.elapsed_time(e1) * 1e3),
+                "start_p50": _pct(rel[:, 0], 50), "start_p90": _pct(rel[:, 0], 90), "start_max": float(rel[:, 0].max()),
+                "prologue_p50": _pct(rel[:, 1], 50), "prologue_p90": _pct(rel[:, 1], 90),
+                "first_rows_p10": _pct(rel[:, 2], 10), "first_rows_p50": _pct(rel[:, 2], 50),
+                "first_rows_p90": _pct(rel[:, 2], 90),
+                "wg_end_min": float(wg_end.min()), "wg_end_p10": _pct(wg_end, 10), "wg_end_p50": _pct(wg_end, 50),
+                "wg_end_p90": _pct(wg_end, 90), "end": float(rel[:, 3].max()),
+            })
+    for pair in mats:
+        for m in pair:
+            m.close()
+    return {"launches": launches}
+
+
+def summary(res: dict) -> str:
+    import numpy as np
+    ls = res["launches"]
+    bytes_launch = 2 * FFN * (HIDDEN // 256) * 144 + 4 * (HIDDEN + 2 * FFN)
+
+    def med(k):
+        return float(np.median([d[k] for d in ls]))
+    walk = med("wg_end_p50") - med("first_rows_p50")
+    rows = [
+        ("HIP-event duration of the eager launch", med("event_us")),
+        ("waves started: median / p90 / last", f"{med('start_p50'):.2f} / {med('start_p90'):.2f} / {med('start_max'):.2f}"),
+        ("x prologue done (barrier): median / p90", f"{med('prologue_p50'):.2f} / {med('prologue_p90'):.2f}"),
+        ("first row group landed: p10 / median / p90",
+         f"{med('first_rows_p10'):.2f} / {med('first_rows_p50'):.2f} / {med('first_rows_p90'):.2f}"),
+        ("workgroup walk end: first / p10 / median / p90",
+         f"{med('wg_end_min'):.2f} / {med('wg_end_p10'):.2f} / {med('wg_end_p50'):.2f} / {med('wg_end_p90'):.2f}"),
+        ("last wave done", med("end")),
+        ("steady-state rate: bytes / (median end - median first rows), TB/s", bytes_launch / (walk * 1e-6) / 1e12),
+    ]
+    out = ["| quantity (µs from the launch's first wave start) | value |", "|---|---:|"]
+    for k, v in rows:
+        out.append(f"| {k} | {v if isinstance(v, str) else f'{v:.2f}'} |")
+    out.append("")
+    out.append(f"{len(ls)} launches ({LAYERS} layers' distinct weights x {REPS}), "
+               f"{ls[0]['waves']} waves each; medians over launches.")
+    return "\n".join(out)
+
+
+def main(argv) -> None:
+    cmd = argv[1] if len(argv) > 1 else "run"
+    if cmd == "build":
+        print(build())
+        return
+    if cmd == "child":
+        print(json.dumps(run_child()))
+        return
+    if not os.path.exists(LIB):
+        raise SystemExit(f"{LIB} is not built: run `python -m juno_amd.timeline build` first")
+    env = dict(os.environ, JUNO_LIB_PATH=LIB, JH_EXTRA_FLAGS=FLAGS)
+    r = subprocess.run([sys.executable, "-m", "juno_amd.timeline", "child"], env=env, capture_output=True, text=True,
+                       cwd=os.path.dirname(HERE))
+    if r.returncode:
+        raise SystemExit(r.stderr[-4000:])
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    print(summary(res))
+    if len(argv) > 2:
+        with open(argv[2], "w") as f:
+            json.dump(res, f, indent=1)
+
+
+if __name__ == "__main__":
+    main(sys.argv)
