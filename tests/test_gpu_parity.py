@@ -641,3 +641,41 @@ def test_batched_swiglu_dev(be, qt, rows, cols, B):
     finally:
         g.close()
         u.close()
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q6_K, O.Q8_0])
+def test_empty_and_edge_ranges(be, qtype):
+    """Edge cases of the matVec contract (LlamaTransformerHandler.matVec's row
+    range, :1200-1212): an empty row range returns an empty vector, B = 0 an
+    empty batch, the first and last single rows match the oracle, a matrix of
+    zero rows uploads and multiplies to nothing, and grouped calls with n = 0
+    are no-ops."""
+    import ctypes
+
+    from juno_amd import _lib
+    rows, cols = 300, 512
+    raw = O.quantize(qtype, weights(rows * cols, 140 + qtype))
+    x = vec(cols, 141)
+    deq = O.dequantize(qtype, raw, rows, cols)
+    with upload(be, qtype, raw, rows, cols) as dev:
+        for k in (0, 17, rows):
+            assert be.sgemv_quant(dev, x, k, k).shape == (0,)
+            assert be.sgemv_batched(dev, np.zeros((4, cols), np.float32), k, k).shape == (4, 0)
+        assert be.sgemv_batched(dev, np.zeros((0, cols), np.float32)).shape == (0, rows)
+        for a in (0, rows - 1):
+            y = be.sgemv_quant(dev, x, a, a + 1)
+            ref = O.matvec(qtype, raw, x, a, a + 1, cols).astype(np.float64)
+            assert rel_err(y, ref, deq[a:a + 1], x).max() <= TOL
+            Y = be.sgemv_batched(dev, np.stack([x, -x, 2 * x, x]), a, a + 1)
+            assert rel_err(Y[1], -ref, deq[a:a + 1], x).max() <= TOL
+            assert rel_err(Y[2], 2 * ref, deq[a:a + 1], x).max() <= TOL
+        with pytest.raises(mv.IllegalArgumentException, match="row range"):
+            be.sgemv_quant(dev, x, 5, 4)
+        with pytest.raises(mv.IllegalArgumentException, match="row range"):
+            be.sgemv_quant(dev, x, 0, rows + 1)
+    with upload(be, qtype, np.zeros(0, np.uint8), 0, cols) as empty:
+        assert be.sgemv_quant(empty, x).shape == (0,)
+        assert be.sgemv_batched(empty, np.stack([x] * 8)).shape == (8, 0)
+    L = _lib.load()
+    assert L.jh_qmatvec_group_dev(0, None, None, None, None) == 0
+    assert L.jh_qmatvec_batched_group_dev(0, None, None, 32, None, None) == 0
