@@ -34,6 +34,7 @@
 #include "jh_kernels.hpp"
 
 #include <mutex>
+#include <stdlib.h>
 
 namespace jh {
 namespace {
@@ -1232,6 +1233,13 @@ static bool plan_group(int n, const MfmaDesc *d, int B, Plan &p) {
             best = cost;
             p.ksb = ksb;
             p.ksplit = kse;
+        }
+    }
+    if (const char *f = getenv("JUNO_MFMA_KSPLIT")) {  // tuning runs: a forced split
+        const int want = atoi(f);
+        if (want >= 1 && want <= p.nsb && (want == 1 || tiles <= kMaxTileCounters)) {
+            p.ksb = (p.nsb + want - 1) / want;
+            p.ksplit = (p.nsb + p.ksb - 1) / p.ksb;
         }
     }
     p.grid = tiles * p.ksplit;
