@@ -208,11 +208,14 @@ int jh_sync_faults(int device, unsigned int *count);
 
 /* Timeline builds only (compiled with -DJH_TIMELINE by juno_amd/timeline.py,
  * never the shipped library; JH_EUNSUPPORTED otherwise): n entries of the
- * staged B = 1 walk's per-wave s_memrealtime stamps (100 MHz) of the last
- * launch, 4 per wave at (workgroup * 16 + wave) * 4: entry, after the x
- * prologue, first row group landed, end of the walk.  No counterpart in the
- * reference; a profiling aid. */
-int jh_debug_timeline(int device, uint64_t *out, size_t n);
+ * per-wave s_memrealtime stamps (100 MHz) of the last launch.  kernel 0: the
+ * staged B = 1 walk, 4 per wave at (workgroup * 16 + wave) * 4: entry, after
+ * the x prologue, first row group landed, end of the walk.  kernel 1: the
+ * batched MFMA walk at B <= 32, 65 per wave at (workgroup * 8 + wave) * 65:
+ * entry, then per super-block step (up to 16) after the barrier, weights
+ * parked, next x staged, MFMAs folded.  No counterpart in the reference; a
+ * profiling aid. */
+int jh_debug_timeline(int device, int kernel, uint64_t *out, size_t n);
 
 /* The attention input norm fused into the grouped GEMV of the matrices that
  * read it: h = x + res, x_out = h (when not NULL; it must not alias x or res),
@@ -314,6 +317,20 @@ int jh_rope_attention_dev(const float *q, const float *k, const float *v, int n_
                           const int *d_pos, int max_seq, float theta, float *k_cache, float *v_cache, float *out,
                           void *stream);
 
+/* jh_rope_attention_dev followed by the output projection y = wo . att
+ * (transformerLayer :765-776: rope, KV append, gqa, then wo): the pair of
+ * calls (jh_rope_attention_dev, then jh_qmatvec_group_dev of wo).  With
+ * JUNO_ATTN_FUSE=1, where the staged GEMV applies (B = 1, at most 64 heads and
+ * 64 chunks of the cache), attention's combine of its chunk partials runs in
+ * the GEMV's input conversion instead of a launch of its own and one of its
+ * workgroups stores att (one launch fewer, but slower at the shapes measured:
+ * each workgroup reads every partial).  att is the attention output either
+ * way, equal bit for bit; y is within the GEMV tolerance of the pair's (the
+ * same bits as the staged kernel on att).  wo has n_heads * head_dim columns.
+ * Same workspace as jh_rope_attention_dev. */
+int jh_rope_attention_qmatvec_dev(const float *q, const float *k, const float *v, int n_heads, int n_kv_heads,
+                                  int head_dim, const int *d_pos, int max_seq, float theta, float *k_cache,
+                                  float *v_cache, const jh_qmat *wo, float *att, float *y, void *stream);
 /* jh_rope_attention_dev for `batch` requests in one launch pair: q [batch][n_heads*head_dim], k and v
  * [batch][n_kv_heads*head_dim], out like q; request z is at position d_pos[z] and uses KV-cache slot
  * d_slot[z] of caches laid out [n_slots][max_seq][n_kv_heads*head_dim] (one slot per request, the

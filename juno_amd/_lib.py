@@ -41,7 +41,7 @@ SIGNATURES = {
     "jh_qmatvec_batched_noalloc_dev": (_I, [_P, _P, _I, _P, _I, _I, _P]),
     "jh_qmatvec_group_dev": (_I, [_I, _P, _P, _P, _P]),
     "jh_sync_faults": (_I, [_I, _P]),
-    "jh_debug_timeline": (_I, [_I, _P, ctypes.c_size_t]),
+    "jh_debug_timeline": (_I, [_I, _I, _P, ctypes.c_size_t]),
     "jh_qmatvec_batched_plan_shape": (_I, [_I, _I, _I, _I, _I, _P, _P]),
     "jh_qmatvec_batched_group_dev": (_I, [_I, _P, _P, _I, _P, _P]),
     "jh_qmatvec_swiglu_dev": (_I, [_P, _P, _P, _P, _P]),
@@ -56,6 +56,7 @@ SIGNATURES = {
     "jh_rope_kv_dev": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P]),
     "jh_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, _P, _P]),
     "jh_rope_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _P]),
+    "jh_rope_attention_qmatvec_dev": (_I, [_P, _P, _P, _I, _I, _I, _P, _I, ctypes.c_float, _P, _P, _P, _P, _P, _P]),
     "jh_silu_mul_dev": (_I, [_P, _P, _I, _P, _P]),
     "jh_pos_increment_dev": (_I, [_P, _I, _P]),
     "jh_embed_dev": (_I, [_P, _P, _P, _P]),

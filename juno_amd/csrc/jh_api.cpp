@@ -795,11 +795,13 @@ int jh_qmatvec_swiglu_dev(const jh_qmat *gate, const jh_qmat *up, const float *d
     return ok();
 }
 
-int jh_debug_timeline(int device, uint64_t *out, size_t n) {
+int jh_debug_timeline(int device, int kernel, uint64_t *out, size_t n) {
     if (!out && n) return fail(JH_EINVAL, "out must not be null");
+    if (kernel != 0 && kernel != 1) return fail(JH_EINVAL, "kernel=%d: 0 (staged walk) or 1 (batched MFMA)", kernel);
     int rc;
     if ((rc = set_device(device))) return rc;
-    const hipError_t e = jh::timeline_read(reinterpret_cast<unsigned long long *>(out), n);
+    const hipError_t e = kernel == 0 ? jh::timeline_read(reinterpret_cast<unsigned long long *>(out), n)
+                                     : jh::mfma_timeline_read(reinterpret_cast<unsigned long long *>(out), n);
     if (e == hipErrorNotSupported) return fail(JH_EUNSUPPORTED, "not a timeline build (-DJH_TIMELINE)");
     if (e != hipSuccess) return hip_fail("timeline read", e);
     return ok();
@@ -1075,6 +1077,66 @@ int jh_rope_attention_batched_dev(const float *q, const float *k, const float *v
                                         true, out, ws, (hipStream_t)stream, batch, d_slot, n_slots);
     if (e != hipSuccess) return hip_fail("attention launch", e);
     return ok();
+}
+
+// JUNO_ATTN_FUSE=1 moves attention's combine into the output projection's
+// input conversion.  Not the default: every workgroup of the GEMV then reads all
+// of the chunk partials (8B, position 511: 266 KB per CU against 37 KB of
+// weights), and the projection takes the staged kernel; measured on MI355X, the
+// 8B decode step went 2.071 -> 2.180 ms and the TinyLlama one 0.857 -> 0.936 ms.
+static bool attn_fuse_wanted() {
+    static const bool on = [] {
+        const char *v = getenv("JUNO_ATTN_FUSE");
+        return v && v[0] == '1';
+    }();
+    return on;
+}
+
+int jh_rope_attention_qmatvec_dev(const float *q, const float *k, const float *v, int n_heads, int n_kv_heads,
+                                  int head_dim, const int *d_pos, int max_seq, float theta, float *k_cache,
+                                  float *v_cache, const jh_qmat *wo, float *d_att, float *d_y, void *stream) {
+    int rc;
+    if ((rc = check_heads(n_heads, n_kv_heads, head_dim, max_seq))) return rc;
+    if ((rc = check_qmat(wo))) return rc;
+    if (!q || !k || !v || !d_pos || !k_cache || !v_cache || !d_att || !d_y)
+        return fail(JH_EINVAL, "pointers must not be null");
+    if ((long long)wo->cols != (long long)n_heads * head_dim)
+        return fail(JH_EINVAL, "wo has %d columns, attention gives n_heads * head_dim = %lld", wo->cols,
+                    (long long)n_heads * head_dim);
+    int dev = 0;
+    JH_HIP("hipGetDevice", hipGetDevice(&dev));
+    void *ws = nullptr;
+    if ((rc = stream_workspace(dev, (hipStream_t)stream, jh::attention_workspace_bytes(n_heads, head_dim, max_seq, 1),
+                               &ws)))
+        return rc;
+    hipStream_t s = (hipStream_t)stream;
+    int tc = 0, nch = 0;
+    jh::attention_chunking(n_heads, n_kv_heads, head_dim, max_seq, 1, &tc, &nch);
+    jh::GemvArgs a;
+    a.type = wo->type;
+    a.w = wo->d_raw;
+    a.pitch = wo->pitch;
+    a.cols = wo->cols;
+    a.row_start = 0;
+    a.row_end = wo->rows;
+    a.batch = 1;
+    a.x = nullptr;
+    a.ldx = wo->cols;
+    a.y = d_y;
+    a.ldy = wo->rows;
+    const jh::CombineSpec cs{static_cast<const float *>(ws), d_pos, head_dim, tc, max_seq, nch, d_att};
+    const bool fuse = wo->type != JH_TYPE_F32 && gemv_path() != 1 && attn_fuse_wanted() && wo->rows > 0 &&
+                      jh::launch_gemv_staged_combine(a, cs, s, true) == hipSuccess;
+    hipError_t e = jh::launch_attention(q, k, v, k_cache, v_cache, n_heads, n_kv_heads, head_dim, d_pos, max_seq, theta,
+                                        true, d_att, ws, s, 1, nullptr, 1, !fuse);
+    if (e != hipSuccess) return hip_fail("attention launch", e);
+    if (fuse) {
+        const MatVecRange range(backend_label(wo->type), wo->rows, wo->cols, 1);
+        e = jh::launch_gemv_staged_combine(a, cs, s);
+        if (e != hipSuccess) return hip_fail("gemv_staged (attention combine) launch", e);
+        return ok();
+    }
+    return jh_qmatvec_group_dev(1, &wo, (const float *const *)&d_att, &d_y, stream);
 }
 
 int jh_attention_dev(const float *q, const float *k_cache, const float *v_cache, int n_heads, int n_kv_heads,

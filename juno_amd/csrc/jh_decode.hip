@@ -644,7 +644,7 @@ __global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ 
     __syncthreads();
     if (tid == 0) {
         float L = 0.f;
-        for (int c = 0; c < nch; c++) L += wl[c] * wc[c];
+        for (int c = 0; c < nch; c++) L = fmaf(wl[c], wc[c], L);
         sL = L;
     }
     __syncthreads();
@@ -658,9 +658,9 @@ __global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ 
 #pragma unroll
             for (int u = 0; u < 8; u++) v[u] = op[(c + u) * (head_dim + 2)];
 #pragma unroll
-            for (int u = 0; u < 8; u++) o += v[u] * wc[c + u];
+            for (int u = 0; u < 8; u++) o = fmaf(v[u], wc[c + u], o);
         }
-        for (; c < nch; c++) o += op[c * (head_dim + 2)] * wc[c];
+        for (; c < nch; c++) o = fmaf(op[c * (head_dim + 2)], wc[c], o);
         out[(size_t)h * head_dim + d] = o / L;
     }
 }
@@ -749,6 +749,22 @@ static bool attn_rv_wanted() {
 // 29.5 us, and at B = 1)
 static bool attn_v_global(int head_dim, int batch) { return head_dim == 128 && batch >= 8; }
 
+static bool attn_rv_applies(int n_heads, int n_kv_heads, int head_dim) {
+    const int R = n_heads / n_kv_heads;
+    return (head_dim == 64 || head_dim == 128) && (R == 1 || R == 2 || R == 4 || R == 8) && attn_rv_wanted();
+}
+// 32-position chunks when the grid would be small (one request): twice the workgroups, each half the rows
+static bool attn_small_chunks(bool rv, int n_kv_heads, int max_seq, int batch) {
+    return rv && (size_t)batch * n_kv_heads * ((max_seq + 63) / 64) < 512 &&
+           (max_seq + kAttnSmallTc - 1) / kAttnSmallTc <= 1024;
+}
+
+void attention_chunking(int n_heads, int n_kv_heads, int head_dim, int max_seq, int batch, int *tc, int *nch) {
+    const bool small = attn_small_chunks(attn_rv_applies(n_heads, n_kv_heads, head_dim), n_kv_heads, max_seq, batch);
+    *tc = small ? kAttnSmallTc : attn_tc(head_dim);
+    *nch = (max_seq + *tc - 1) / *tc;
+}
+
 size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq, int batch) {
     const int tc = head_dim <= 128 ? kAttnSmallTc : attn_tc(head_dim);  // the finest chunking the launcher may pick
     const int nch = (max_seq + tc - 1) / tc;
@@ -758,12 +774,10 @@ size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq, int bat
 hipError_t launch_attention(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
                             int n_heads, int n_kv_heads, int head_dim, const int *d_pos, int max_seq, float theta,
                             bool fused, float *out, void *workspace, hipStream_t s, int batch, const int *d_slot,
-                            int n_slots) {
+                            int n_slots, bool combine) {
     const int R = n_heads / n_kv_heads;
-    const bool rv = (head_dim == 64 || head_dim == 128) && (R == 1 || R == 2 || R == 4 || R == 8) && attn_rv_wanted();
-    // 32-position chunks when the grid would be small (one request): twice the workgroups, each half the rows
-    const bool small = rv && (size_t)batch * n_kv_heads * ((max_seq + 63) / 64) < 512 &&
-                       (max_seq + kAttnSmallTc - 1) / kAttnSmallTc <= 1024;
+    const bool rv = attn_rv_applies(n_heads, n_kv_heads, head_dim);
+    const bool small = attn_small_chunks(rv, n_kv_heads, max_seq, batch);
     const int tc = small ? kAttnSmallTc : attn_tc(head_dim), nch = (max_seq + tc - 1) / tc;
     if (nch > 1024) return hipErrorNotSupported;  // combine weights live in a fixed LDS array
     const float scale = (float)(1.0 / sqrt((double)head_dim));
@@ -843,7 +857,7 @@ hipError_t launch_attention(const float *q, const float *k_new, const float *v_n
         attn_chunk_k<false><<<grid, 64 * nw, lds, s>>>(q, nullptr, nullptr, k_cache, v_cache, n_heads, n_kv_heads, head_dim,
                                                  d_pos, max_seq, theta, scale, part, d_slot, n_slots);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || !combine) return e;
     attn_combine_k<<<dim3(n_heads, batch), 256, 0, s>>>(part, head_dim, tc, d_pos, max_seq, nch, out);
     return hipGetLastError();
 }

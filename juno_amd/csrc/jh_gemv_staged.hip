@@ -575,7 +575,24 @@ struct StagedArgs {
     const float *res, *norm_w;
     float eps;
     float *x_out;
+    // attention-combine prologue (COMB kernels): x is the log-sum-exp merge of
+    // the chunk partials attn_part ([head][attn_nchmax][m, l, o[head_dim]]) of
+    // one request, over the chunks that hold positions 0 .. *attn_pos;
+    // workgroup 0 stores that x to x_out when it is not null
+    const float *attn_part;
+    const int *attn_pos;
+    int attn_hd, attn_tc, attn_max_seq, attn_nchmax;
+    bool dry;  // host only: the launcher checks that the kernel applies and launches nothing
 };
+
+// COMB: the prologue's LDS after the walk's (claim counter, per-wave flags):
+// chunk weights [heads][nchmax], normalisers [heads], then the merged x [cols]
+__host__ __device__ constexpr size_t staged_comb_offset(int nblk, int nw, int r, int ch) {
+    return (staged_front(true, nblk, nw, r, ch) + 4 + 4 * (size_t)nw + 15) & ~size_t(15);
+}
+__host__ __device__ constexpr size_t staged_comb_x(int heads, int nchmax) {
+    return ((size_t)heads * nchmax + heads + 3) & ~size_t(3);  // floats before the merged x
+}
 
 // SwiGLU pairing: virtual row v is row v / 2 of gate (v even) or up (v odd),
 // so that a row group (R even) holds both halves of its outputs.
@@ -598,8 +615,8 @@ __device__ __forceinline__ int staged_problem(const StagedArgs &a, int v) {
 // in another summation order, at a fraction of the walk's speed: it is the
 // path for x with one outlier among many much smaller elements, which the
 // walk's 30-bit fixed point per sub-block does not carry to the GEMV bar.
-template <int T, bool NORM>
-__device__ __forceinline__ void staged_exact(const StagedArgs &args, float nscale) {
+template <int T, bool NORM, bool COMB = false>
+__device__ __forceinline__ void staged_exact(const StagedArgs &args, float nscale, const float *xl = nullptr) {
     constexpr int G = Fmt<T>::G;
     const int lane = threadIdx.x & 63;
     // the wave's index, uniform (readfirstlane): rows and matrices are then chosen
@@ -608,6 +625,7 @@ __device__ __forceinline__ void staged_exact(const StagedArgs &args, float nscal
     const int gwave = __builtin_amdgcn_readfirstlane((int)blockIdx.x * waves + (int)(threadIdx.x >> 6));
     const int units = args.cols / G;
     auto xat = [&](int64_t c) {
+        if constexpr (COMB) return xl[c];  // the merged x in LDS
         return NORM ? (args.norm_w[c] * (args.x[c] + args.res[c])) * nscale : args.x[c];
     };
     auto row_dot = [&](int vr) {
@@ -636,12 +654,14 @@ __device__ __forceinline__ void staged_exact(const StagedArgs &args, float nscal
 
 // SX: one column tile, x shared through an LDS image; NW: waves per workgroup;
 // NORM: x is the residual add and rmsnorm of the arguments (SX only)
+// COMB: x is attention's combine of its chunk partials (SX, DYN, every block
+// of x converted in the waves' first pass)
 // DYN (one column tile only): the workgroup takes a contiguous range of row
 // groups and its waves claim them one at a time from an LDS counter.  Waves
 // sharing a CU do not progress at one rate (the oldest issue first), so equal
 // static shares leave a CU with its last waves running alone; claimed groups
 // even that out.
-template <int T, int R, bool SX, int NW, bool NORM = false, bool DYN = false>
+template <int T, int R, bool SX, int NW, bool NORM = false, bool DYN = false, bool COMB = false>
 __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     using F = Fmt<T>;
     constexpr int K = (F::CH + 63) / 64;  // 16-byte loads per lane per row
@@ -708,7 +728,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
 #pragma unroll
         for (int k = 0; k < NXS; k++) {
             const int c = (wave + NW * k) * 256 + lane * 4;
-            xv[k] = x_load4(args.x, args.cols, c);
+            if constexpr (!COMB) xv[k] = x_load4(args.x, args.cols, c);
             if constexpr (NORM) {
                 rv[k] = x_load4(args.res, args.cols, c);
                 nwv[k] = x_load4(args.norm_w, args.cols, c);
@@ -786,6 +806,88 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
             xv[k] = make_float4(nwv[k].x * xv[k].x * scale, nwv[k].y * xv[k].y * scale, nwv[k].z * xv[k].z * scale,
                                 nwv[k].w * xv[k].w * scale);
     }
+    float *cmb_x = nullptr;  // COMB: the merged x in LDS (the exact path reads it)
+    if constexpr (COMB) {
+        // attn_combine_k's arithmetic in its order (gqa, LlamaTransformerHandler.java:1678-1731):
+        // per head, M = the chunks' largest score, weights exp(m_c - M) (double),
+        // L = sum_c l_c w_c in chunk order, x[d] = (sum_c o_c[d] w_c in chunk order) / L
+        const int hd = args.attn_hd, nh = args.cols / hd, nchmax = args.attn_nchmax, stride = hd + 2;
+        float *wcl = reinterpret_cast<float *>(lds + staged_comb_offset(nblk, NW, R, F::CH));
+        float *Ll = wcl + nh * nchmax;
+        cmb_x = wcl + staged_comb_x(nh, nchmax);
+        const int npos = min(*args.attn_pos, args.attn_max_seq - 1) + 1;
+        const int nch = min((npos + args.attn_tc - 1) / args.attn_tc, nchmax);
+        // a. wave w takes heads w, w + NW, ..: lane c holds chunk c's (m, l)
+        constexpr int HW = 4;  // heads per wave (the launcher admits at most 4 NW)
+        float mv[HW], lv[HW];
+#pragma unroll
+        for (int j = 0; j < HW; j++) {
+            const int h = min(wave + NW * j, nh - 1), c = min(lane, nch - 1);
+            const float *ph = args.attn_part + ((size_t)h * nchmax + c) * stride;
+            mv[j] = ph[0];
+            lv[j] = ph[1];
+        }
+#pragma unroll
+        for (int j = 0; j < HW; j++) {
+            const int h = wave + NW * j;
+            if (h >= nh) break;  // uniform over the wave
+            const bool in = lane < nch;
+            float M = in ? mv[j] : -INFINITY;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+            const float w = in ? (float)exp((double)(mv[j] - M)) : 0.f;
+            if (in) wcl[h * nchmax + lane] = w;
+            float L = 0.f;
+            for (int c = 0; c < nch; c++)
+                L = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv[j]), c)),
+                         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c)), L);
+            if (lane == 0) Ll[h] = L;
+        }
+        __syncthreads();
+        // b. this wave's blocks: lane's 4 columns (one head) merged over the chunks
+#pragma unroll
+        for (int k = 0; k < NXS; k++) {
+            const int c0 = (wave + NW * k) * 256 + lane * 4;
+            if (c0 >= args.cols) {
+                xv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                continue;
+            }
+            const int h = c0 / hd, d = c0 - h * hd;
+            const float *op = args.attn_part + (size_t)h * nchmax * stride + 2 + d;
+            const float *wh = wcl + h * nchmax;
+            float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+            int c = 0;
+            for (; c + 8 <= nch; c += 8) {
+                float2 a[8], b[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    a[u] = *reinterpret_cast<const float2 *>(op + (size_t)(c + u) * stride);
+                    b[u] = *reinterpret_cast<const float2 *>(op + (size_t)(c + u) * stride + 2);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const float wc = wh[c + u];
+                    o0 = fmaf(a[u].x, wc, o0);
+                    o1 = fmaf(a[u].y, wc, o1);
+                    o2 = fmaf(b[u].x, wc, o2);
+                    o3 = fmaf(b[u].y, wc, o3);
+                }
+            }
+            for (; c < nch; c++) {
+                const float2 a = *reinterpret_cast<const float2 *>(op + (size_t)c * stride);
+                const float2 b = *reinterpret_cast<const float2 *>(op + (size_t)c * stride + 2);
+                const float wc = wh[c];
+                o0 = fmaf(a.x, wc, o0);
+                o1 = fmaf(a.y, wc, o1);
+                o2 = fmaf(b.x, wc, o2);
+                o3 = fmaf(b.y, wc, o3);
+            }
+            const float L = Ll[h];
+            xv[k] = make_float4(o0 / L, o1 / L, o2 / L, o3 / L);
+            *reinterpret_cast<float4 *>(cmb_x + c0) = xv[k];
+            if (blockIdx.x == 0 && args.x_out) *reinterpret_cast<float4 *>(args.x_out + c0) = xv[k];
+        }
+    }
     if constexpr (shared_x) {
         // each wave's flag: whether a group it converted needs the exact path
         bool need = false;
@@ -802,7 +904,7 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
 #pragma unroll
         for (int w = 0; w < NW; w++) anyneed |= xneed[w];
         if (__builtin_amdgcn_readfirstlane(anyneed)) {  // uniform over the workgroup; see residual_matters
-            staged_exact<T, NORM>(args, nscale);
+            staged_exact<T, NORM, COMB>(args, nscale, cmb_x);
             return;
         }
         issue(grp);
@@ -947,9 +1049,9 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
     }
 }
 
-template <int T, int R, bool SX, int NW, bool NORM, bool DYN>
+template <int T, int R, bool SX, int NW, bool NORM, bool DYN, bool COMB = false>
 __global__ __launch_bounds__(64 * NW) void gemv_staged(StagedArgs args) {
-    gemv_staged_body<T, R, SX, NW, NORM, DYN>(args);
+    gemv_staged_body<T, R, SX, NW, NORM, DYN, COMB>(args);
 }
 
 // One-column-tile rows take one workgroup per CU (16 waves of one row, or 12 of
@@ -1020,10 +1122,10 @@ static int resident_workgroups(const void *kern, int threads, size_t lds) {
     return cus * (per_cu > cap ? cap : per_cu);
 }
 
-template <int T, int R, bool SX, int NW, bool NORM = false, bool DYN = false>
+template <int T, int R, bool SX, int NW, bool NORM = false, bool DYN = false, bool COMB = false>
 hipError_t launch_staged_nw(const StagedArgs &sa, int nblk, int ngroups, hipStream_t s) {
     using F = Fmt<T>;
-    const void *kern = reinterpret_cast<const void *>(&gemv_staged<T, R, SX, NW, NORM, DYN>);
+    const void *kern = reinterpret_cast<const void *>(&gemv_staged<T, R, SX, NW, NORM, DYN, COMB>);
     // allow more than the default 64 KB of dynamic LDS (160 KB per CU on gfx950).  The
     // call has been refused for some instantiations: its error is cleared here, so
     // that the launch's own status is the one reported, and such a kernel keeps 64 KB.
@@ -1033,14 +1135,19 @@ hipError_t launch_staged_nw(const StagedArgs &sa, int nblk, int ngroups, hipStre
         return ok ? size_t(160) * 1024 : size_t(64) * 1024;
     }();
     // walk, claim counter, per-wave flags
-    const size_t base = staged_front(SX, nblk, NW, R, F::CH) + 4 + 4 * NW;
+    size_t base = staged_front(SX, nblk, NW, R, F::CH) + 4 + 4 * NW;
+    if (COMB) {
+        const int nh = sa.cols / sa.attn_hd;
+        base = staged_comb_offset(nblk, NW, R, F::CH) + 4 * (staged_comb_x(nh, sa.attn_nchmax) + (size_t)sa.cols);
+    }
     if (base > lds_max) return hipErrorNotSupported;
     const int slots = NW / sa.gw;
     const int need = (ngroups + slots - 1) / slots;
     // persistent grid: as many workgroups as fit at once (DYN: one per CU), capped by the work
     int wgs = DYN ? cu_count() : resident_workgroups(kern, 64 * NW, base);
     if (wgs > need) wgs = need;
-    gemv_staged<T, R, SX, NW, NORM, DYN><<<wgs, 64 * NW, base, s>>>(sa);
+    if (sa.dry) return hipSuccess;
+    gemv_staged<T, R, SX, NW, NORM, DYN, COMB><<<wgs, 64 * NW, base, s>>>(sa);
     return hipGetLastError();
 }
 
@@ -1052,6 +1159,10 @@ hipError_t launch_staged_t(StagedArgs sa, hipStream_t s) {
     sa.tb = (nb + sa.gw - 1) / sa.gw;
     const int nblk = (sa.cols + 255) / 256;
     const int ngroups = (sa.nrows + R - 1) / R;
+    if (sa.attn_part) {  // one pass of 16 waves converts every block; one row per group
+        if (sa.gw != 1 || nblk > 16 || R != 1 || !staged_dyn()) return hipErrorNotSupported;
+        return launch_staged_nw<T, 1, true, 16, false, true, true>(sa, nblk, ngroups, s);
+    }
     if (sa.norm_w) {  // the rmsnorm prologue needs the shared image and every block in one pass of the waves
         if (sa.gw != 1 || nblk > 16) return hipErrorNotSupported;
         if (staged_dyn()) {
@@ -1155,6 +1266,9 @@ static hipError_t launch_staged_any(const StagedArgs &sa, int type, hipStream_t 
 constexpr size_t kStagedMinBytes = 28u << 20;
 constexpr size_t kStagedMinWideBytes = 16u << 20;
 constexpr size_t kStagedMinFusedBytes = 8u << 20;
+// With attention's combine in the prologue the launch also saves the combine's
+// launch; JUNO_STAGED_MIN_COMB (MB) overrides this for tuning runs.
+constexpr size_t kStagedMinCombBytes = 0;
 
 // Thresholds in MB: JUNO_STAGED_MIN (one column tile), JUNO_STAGED_MIN_WIDE
 // (column-tiled rows) and JUNO_STAGED_MIN_FUSED (with the rmsnorm prologue)
@@ -1198,6 +1312,36 @@ hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s, const NormSpec *
     sa.cols = a.cols;
     sa.x = a.x;
     set_norm(sa, norm);
+    return launch_staged_any(sa, a.type, s);
+}
+
+hipError_t launch_gemv_staged_combine(const GemvArgs &a, const CombineSpec &c, hipStream_t s, bool check_only) {
+    if (a.batch != 1 || !staged_supported(a.type, a.cols) || a.cols % 256 || c.head_dim < 4 || c.head_dim % 4 ||
+        a.cols % c.head_dim || a.cols / c.head_dim > 4 * 16 || c.nchmax < 1 || c.nchmax > 64 || c.tc < 1)
+        return hipErrorNotSupported;
+    const int nrows = a.row_end - a.row_start;
+    static const size_t comb_min = env_mb("JUNO_STAGED_MIN_COMB", kStagedMinCombBytes);
+    if ((size_t)nrows * a.pitch < comb_min && !getenv("JUNO_STAGED_R")) return hipErrorNotSupported;
+    StagedArgs sa = {};
+    sa.np = 1;
+    sa.w[0] = a.w;
+    sa.y[0] = a.y;
+    sa.row0[0] = a.row_start;
+    sa.cum[0] = 0;
+    sa.cum[1] = nrows;
+    sa.pitch = a.pitch;
+    sa.nb = a.type == 8 ? a.cols / 32 : a.cols / 256;
+    sa.nrows = nrows;
+    sa.cols = a.cols;
+    sa.x = nullptr;
+    sa.x_out = c.x_out;
+    sa.attn_part = c.part;
+    sa.attn_pos = c.pos;
+    sa.attn_hd = c.head_dim;
+    sa.attn_tc = c.tc;
+    sa.attn_max_seq = c.max_seq;
+    sa.attn_nchmax = c.nchmax;
+    sa.dry = check_only;
     return launch_staged_any(sa, a.type, s);
 }
 

@@ -74,11 +74,25 @@ hipError_t launch_gemv_swiglu(const GroupProblem &gate, const GroupProblem &up, 
 hipError_t sync_faults(unsigned *count);
 // Timeline builds only (-DJH_TIMELINE): the staged walk's per-wave timestamps.
 hipError_t timeline_read(unsigned long long *out, size_t n);
+hipError_t mfma_timeline_read(unsigned long long *out, size_t n);
 
 // B = 1 coalesced, pipelined, int8-x kernel (jh_gemv_staged.hip); returns
 // hipErrorNotSupported for shapes it does not cover.
 bool staged_supported(int type, int cols);
 hipError_t launch_gemv_staged(const GemvArgs &a, hipStream_t s, const NormSpec *norm = nullptr);
+// The input of a B = 1 GEMV formed in the staged kernel's prologue as attention's
+// combine of its chunk partials (launch_attention with combine = false): part
+// holds [head][nchmax][m, l, o[head_dim]] for heads = cols / head_dim, over the
+// chunks of tc positions that hold 0 .. *pos.  Workgroup 0 stores the merged x
+// to x_out (may be null).  hipErrorNotSupported where it does not apply.
+struct CombineSpec {
+    const float *part;
+    const int *pos;
+    int head_dim, tc, max_seq, nchmax;
+    float *x_out;
+};
+// check_only: hipSuccess when it applies, nothing launched
+hipError_t launch_gemv_staged_combine(const GemvArgs &a, const CombineSpec &c, hipStream_t s, bool check_only = false);
 
 // Batched decode through the LDS-staged, fp16-MFMA path (kMfmaMinBatch <= B <= 64).
 // Batched GEMVs (kMfmaMinBatch <= B <= 64) on fp16 MFMA: up to kMaxMfmaGroup matrices
@@ -144,7 +158,10 @@ size_t attention_workspace_bytes(int n_heads, int head_dim, int max_seq, int bat
 hipError_t launch_attention(const float *q, const float *k_new, const float *v_new, float *k_cache, float *v_cache,
                             int n_heads, int n_kv_heads, int head_dim, const int *d_pos, int max_seq, float theta,
                             bool fused, float *out, void *workspace, hipStream_t s, int batch = 1,
-                            const int *d_slot = nullptr, int n_slots = 1);
+                            const int *d_slot = nullptr, int n_slots = 1, bool combine = true);
+// the chunking launch_attention picks: chunk length *tc, *nch chunks per head
+// cover max_seq (the partials' stride)
+void attention_chunking(int n_heads, int n_kv_heads, int head_dim, int max_seq, int batch, int *tc, int *nch);
 // Arrival counters of the MFMA split-K hand-off: kCounterSlots per stream, one
 // 128-byte line each, so that workgroups arriving at different counters never
 // queue on one line's atomics.  Every launch leaves the counters it used at zero.

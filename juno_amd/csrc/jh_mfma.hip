@@ -50,6 +50,23 @@ typedef uint32_t u32a2 __attribute__((aligned(2)));
 constexpr int kPrefetch = 1;  // super-blocks of weight chunks in flight per wave (B <= 32)
 constexpr int kMinWorkgroups = 256;  // split K until the grid has this many
 
+// Timeline builds (-DJH_TIMELINE, juno_amd/timeline.py; never the shipped
+// library): per wave of the B <= 32 double-buffered walk, s_memrealtime at entry
+// and, per super-block step, after the step's barrier, once its weight chunks
+// are parked, once the next x is staged, and after its MFMAs and fold.
+#ifdef JH_TIMELINE
+constexpr int kMtWg = 512, kMtSteps = 16, kMtPer = 1 + 4 * kMtSteps;
+__device__ unsigned long long g_mtimeline[kMtWg * 8 * kMtPer];
+#define JH_MT(slot)                                                                                         \
+    do {                                                                                                    \
+        if ((threadIdx.x & 63) == 0 && blockIdx.x < kMtWg && (slot) < kMtPer)                               \
+            g_mtimeline[((size_t)blockIdx.x * 8 + (threadIdx.x >> 6)) * kMtPer + (slot)] =                 \
+                __builtin_amdgcn_s_memrealtime();                                                           \
+    } while (0)
+#else
+#define JH_MT(slot) do {} while (0)
+#endif
+
 constexpr int kRowsPerWave = 32;
 constexpr int kWaves = 8;  // waves per workgroup: 256 rows share each staged x slice
 constexpr int kThreads = 64 * kWaves;
@@ -931,6 +948,7 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
                            const_cast<float2 *>(cx.sh_S), xcol, COLH);
         };
         uint8_t *wslot2 = lds + 2 * XS + wave * (kRowsPerWave * RC * 16);
+        JH_MT(0);
         if (sb0 < sb1) {
             JH_LOAD_X(sb0);
             JH_LOAD_W(0, sb0);
@@ -940,9 +958,11 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
         for (int sb = sb0; sb < sb1; sb++) {
             const int buf = (sb - sb0) & 1;
             __syncthreads();  // x of sb is staged; the other buffer is free
+            JH_MT(1 + 4 * (sb - sb0));
 #pragma unroll
             for (int k = 0; k < CL; k++)
                 if (lane + 64 * k < kRowsPerWave * CH) *reinterpret_cast<u32x4 *>(wslot2 + 16 * win_chunk<CH, RC>(lane + 64 * k)) = ch_n[0][k];
+            JH_MT(2 + 4 * (sb - sb0));
             typename F::Regs w;
             F::template load<true>(w, wslot2 + c.lr * RC * 16 + ((myoff + (size_t)sb * F::kBytes) & 15), c.kh);
             if (sb + 1 < sb1) {
@@ -950,7 +970,9 @@ __device__ __forceinline__ void gemm_body(const MfmaProblem &P, int tile, int sp
                 if (sb + 2 < sb1) JH_LOAD_X(sb + 2);
                 JH_LOAD_W(0, sb + 1);
             }
+            JH_MT(3 + 4 * (sb - sb0));
             fold(w, ctx_at(buf));
+            JH_MT(4 + 4 * (sb - sb0));
         }
     } else {
     if (sb0 < sb1) JH_LOAD_X(sb0);
@@ -1424,6 +1446,17 @@ hipError_t launch_mfma_group(int n, const MfmaDesc *d, int B, void *workspace, i
     if (B <= 32) launch_group_nt<1>(g, mask, p.grid, s);
     else launch_group_nt<2>(g, mask, p.grid, s);
     return hipGetLastError();
+}
+
+hipError_t mfma_timeline_read(unsigned long long *out, size_t n) {
+#ifdef JH_TIMELINE
+    if (n > (size_t)kMtWg * 8 * kMtPer) n = (size_t)kMtWg * 8 * kMtPer;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_mtimeline), n * sizeof(unsigned long long));
+#else
+    (void)out;
+    (void)n;
+    return hipErrorNotSupported;
+#endif
 }
 
 }  // namespace jh

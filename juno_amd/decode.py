@@ -321,10 +321,11 @@ class LlamaDecoder:
                     ad = self.lora.get(li, proj)
                     if ad is not None:
                         ad.apply_dev(self.xn.data_ptr(), out.data_ptr(), 1, stream)
-            # rope on q and k, KV append and gqa (:765-773) in one launch pair
-            _check(L.jh_rope_attention_dev(P(self.q), P(self.k), P(self.v), nh, nkv, hd, P(self.pos), self.max_seq,
-                                           c.rope_theta, P(self.k_cache[li]), P(self.v_cache[li]), P(self.att), s))
-            self._group([m["o"]], [self.att], [self.proj], s)
+            # rope on q and k, KV append, gqa (:765-773) and the output projection (:776): the
+            # attention combine runs in the projection's input conversion where that applies
+            _check(L.jh_rope_attention_qmatvec_dev(P(self.q), P(self.k), P(self.v), nh, nkv, hd, P(self.pos),
+                                                   self.max_seq, c.rope_theta, P(self.k_cache[li]),
+                                                   P(self.v_cache[li]), m["o"].handle, P(self.att), P(self.proj), s))
             # x2 = x + attnProj (:778), rmsNorm(x2) (:781) and silu(gate . x2n) * (up . x2n) (:796-797):
             # where the staged kernel applies, one launch (the norm in its input conversion, each gate row
             # paired with its up row); else the norm into xn and the paired GEMV

@@ -6,6 +6,8 @@ GPU box:
 
     python -m juno_amd.timeline build    # juno_amd/_timeline/libjunohip.so, compiled with -DJH_TIMELINE
     python -m juno_amd.timeline run      # the launches and the summary (markdown on stdout)
+    python -m juno_amd.timeline mfma     # the same for the batched MFMA walk, B = 32
+
 
 The instrumented build stamps s_memrealtime (100 MHz) per wave of the DYN walk
 at entry, after the x prologue's barrier, once its first row group has landed
@@ -83,7 +85,7 @@ def run_child() -> dict:
                 raise RuntimeError(_lib.last_error())
             e1.record(s)
             torch.cuda.synchronize()
-            if L.jh_debug_timeline(0, buf, n_slots):
+            if L.jh_debug_timeline(0, 0, buf, n_slots):
                 raise RuntimeError(_lib.last_error())
             if rep == 0:
                 continue  # warm-up pass
@@ -106,6 +108,103 @@ def run_child() -> dict:
         for m in pair:
             m.close()
     return {"launches": launches}
+
+
+def run_child_mfma(B: int = 32) -> dict:
+    """The grouped [gate, up] MFMA launch at batch B: per wave and super-block
+    step, time waiting at the step's barrier, parking the weight chunks (waits
+    on their global loads), staging the next x (and issuing the next loads), and
+    the MFMAs plus the fold."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from juno_amd import _lib
+    from juno_amd import matvec as mv
+
+    L = _lib.load()
+    be = mv.GpuContext.shared(0).create_mat_vec()
+    s = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    mats = []
+    for _ in range(LAYERS):
+        pair = []
+        for _ in range(2):
+            w = torch.randn(FFN * HIDDEN, generator=g, device="cuda").mul_(0.02)
+            pair.append(be.quantize_dev(mv.Q4_K, w.data_ptr(), FFN, HIDDEN, s.cuda_stream))
+            del w
+        mats.append(pair)
+    torch.cuda.synchronize()
+    X = torch.randn(B, HIDDEN, generator=g, device="cuda")
+    ys = [torch.empty(B, FFN, device="cuda") for _ in range(2)]
+    V = ctypes.c_void_p
+    kernel, ksplit = ctypes.c_int(), ctypes.c_int()
+    hs0 = (V * 2)(mats[0][0].handle, mats[0][1].handle)
+    if L.jh_qmatvec_batched_plan(2, hs0, B, ctypes.byref(kernel), ctypes.byref(ksplit)):
+        raise RuntimeError(_lib.last_error())
+    per = 65
+    n_slots = 512 * 8 * per
+    buf = (ctypes.c_uint64 * n_slots)()
+    launches = []
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for rep in range(REPS + 1):
+        for pair in mats:
+            hs = (V * 2)(pair[0].handle, pair[1].handle)
+            xs = (V * 2)(X.data_ptr(), X.data_ptr())
+            yp = (V * 2)(ys[0].data_ptr(), ys[1].data_ptr())
+            ctypes.memset(buf, 0, ctypes.sizeof(buf))
+            e0.record(s)
+            if L.jh_qmatvec_batched_group_dev(2, hs, xs, B, yp, V(s.cuda_stream)):
+                raise RuntimeError(_lib.last_error())
+            e1.record(s)
+            torch.cuda.synchronize()
+            if L.jh_debug_timeline(0, 1, buf, n_slots):
+                raise RuntimeError(_lib.last_error())
+            if rep == 0:
+                continue
+            t = np.frombuffer(buf, dtype=np.uint64).reshape(-1, per).astype(np.int64)
+            t = t[t[:, 0] > 0]
+            steps = int(((t[:, 1:] > 0).sum(axis=1) // 4).min())
+            base = t[:, 0].min()
+            rel = (t[:, : 1 + 4 * steps] - base) * TICK_NS / 1e3
+            st = rel[:, 1:].reshape(len(rel), steps, 4)
+            prev = np.concatenate([rel[:, :1], st[:, :-1, 3]], axis=1)  # end of the previous step
+            parts = {"barrier": st[:, :, 0] - prev, "park": st[:, :, 1] - st[:, :, 0],
+                     "stage_issue": st[:, :, 2] - st[:, :, 1], "mfma_fold": st[:, :, 3] - st[:, :, 2]}
+            d = {"waves": int(len(rel)), "steps": steps, "event_us": float(e0.elapsed_time(e1) * 1e3),
+                 "start_p50": _pct(rel[:, 0], 50), "start_max": float(rel[:, 0].max()),
+                 "first_step_p50": _pct(st[:, 0, 0], 50), "walk_end_p50": _pct(st[:, -1, 3], 50),
+                 "walk_end_max": float(st[:, -1, 3].max())}
+            for k, v in parts.items():
+                d[k + "_first"] = _pct(v[:, 0], 50)
+                d[k + "_rest"] = _pct(v[:, 1:], 50) if steps > 1 else 0.0
+                d[k + "_rest_p90"] = _pct(v[:, 1:], 90) if steps > 1 else 0.0
+            launches.append(d)
+    for pair in mats:
+        for m in pair:
+            m.close()
+    return {"launches": launches, "B": B, "kernel": kernel.value, "ksplit": ksplit.value}
+
+
+def summary_mfma(res: dict) -> str:
+    import numpy as np
+    ls = res["launches"]
+
+    def med(k):
+        return float(np.median([d[k] for d in ls]))
+    out = [f"B = {res['B']}, plan kernel {res['kernel']} K split {res['ksplit']}, {ls[0]['waves']} waves, "
+           f"{ls[0]['steps']} super-block steps per wave; medians over {len(ls)} launches.", "",
+           "| quantity (µs) | value |", "|---|---:|",
+           f"| HIP-event duration of the eager launch | {med('event_us'):.2f} |",
+           f"| waves started: median / last | {med('start_p50'):.2f} / {med('start_max'):.2f} |",
+           f"| first step's barrier passed (median wave) | {med('first_step_p50'):.2f} |",
+           f"| walk end: median wave / last wave | {med('walk_end_p50'):.2f} / {med('walk_end_max'):.2f} |",
+           "", "| per step, median wave (p90) | first step | later steps |", "|---|---:|---:|"]
+    for k in ("barrier", "park", "stage_issue", "mfma_fold"):
+        out.append(f"| {k} | {med(k + '_first'):.2f} | {med(k + '_rest'):.2f} ({med(k + '_rest_p90'):.2f}) |")
+    return "\n".join(out)
 
 
 def summary(res: dict) -> str:
@@ -144,18 +243,20 @@ def main(argv) -> None:
     if cmd == "child":
         print(json.dumps(run_child()))
         return
+    if cmd == "child_mfma":
+        print(json.dumps(run_child_mfma(int(argv[2]) if len(argv) > 2 else 32)))
+        return
     if not os.path.exists(LIB):
         raise SystemExit(f"{LIB} is not built: run `python -m juno_amd.timeline build` first")
     env = dict(os.environ, JUNO_LIB_PATH=LIB, JH_EXTRA_FLAGS=FLAGS)
-    r = subprocess.run([sys.executable, "-m", "juno_amd.timeline", "child"], env=env, capture_output=True, text=True,
+    mfma = cmd == "mfma"
+    child = ["child_mfma", argv[2] if len(argv) > 2 else "32"] if mfma else ["child"]
+    r = subprocess.run([sys.executable, "-m", "juno_amd.timeline", *child], env=env, capture_output=True, text=True,
                        cwd=os.path.dirname(HERE))
     if r.returncode:
         raise SystemExit(r.stderr[-4000:])
     res = json.loads(r.stdout.strip().splitlines()[-1])
-    print(summary(res))
-    if len(argv) > 2:
-        with open(argv[2], "w") as f:
-            json.dump(res, f, indent=1)
+    print(summary_mfma(res) if mfma else summary(res))
 
 
 if __name__ == "__main__":
