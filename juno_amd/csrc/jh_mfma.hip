@@ -1298,7 +1298,17 @@ static void launch_group_nt(const MfmaGroup &g, int mask, int grid, hipStream_t 
     }
 }
 
+// JUNO_MFMA_PAIR=0: the batched SwiGLU takes the grouped launch and silu_mul (A/B runs)
+static bool mfma_pair_wanted() {
+    static const bool on = [] {
+        const char *v = getenv("JUNO_MFMA_PAIR");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
 bool mfma_swiglu_applies(const MfmaDesc &gate, const MfmaDesc &up, int B) {
+    if (!mfma_pair_wanted()) return false;
     if (B < kMfmaMinBatch || B > 32 || gate.type != up.type || gate.cols != up.cols || gate.pitch != up.pitch ||
         gate.x != up.x || gate.row_start != 0 || up.row_start != 0 || gate.row_end != up.row_end)
         return false;

@@ -6,8 +6,7 @@ GPU box:
 
     python -m juno_amd.timeline build    # juno_amd/_timeline/libjunohip.so, compiled with -DJH_TIMELINE
     python -m juno_amd.timeline run      # the launches and the summary (markdown on stdout)
-    python -m juno_amd.timeline mfma     # the same for the batched MFMA walk, B = 32
-
+    python -m juno_amd.timeline mfma 32  # the batched MFMA walk at B <= 32 (per super-block step)
 
 The instrumented build stamps s_memrealtime (100 MHz) per wave of the DYN walk
 at entry, after the x prologue's barrier, once its first row group has landed
@@ -15,7 +14,10 @@ in LDS, and at the end of its walk (jh_debug_timeline).  The shipped library
 has no stamps (jh_debug_timeline returns JH_EUNSUPPORTED there).  Each launch
 is timed relative to its earliest wave start; the summary gives medians and
 spreads over launches, with the weights of 8 distinct layers so that no launch
-finds its matrices in the 256 MB MALL.
+finds its matrices in the 256 MB MALL.  The MFMA variant stamps each wave of
+the B <= 32 walk at entry and, per super-block step, after the step's barrier,
+once its weight chunks are parked in LDS, once the next x is staged and after
+its MFMAs and fold (jh_debug_timeline kernel 1).
 """
 from __future__ import annotations
 
@@ -257,6 +259,11 @@ def main(argv) -> None:
         raise SystemExit(r.stderr[-4000:])
     res = json.loads(r.stdout.strip().splitlines()[-1])
     print(summary_mfma(res) if mfma else summary(res))
+    # run [json], mfma [B [json]]
+    out = (argv[3] if len(argv) > 3 else None) if mfma else (argv[2] if len(argv) > 2 else None)
+    if out:
+        with open(out, "w") as f:
+            json.dump(res, f, indent=1)
 
 
 if __name__ == "__main__":
