@@ -211,9 +211,10 @@ int jh_sync_faults(int device, unsigned int *count);
  * per-wave s_memrealtime stamps (100 MHz) of the last launch.  kernel 0: the
  * staged B = 1 walk, 4 per wave at (workgroup * 16 + wave) * 4: entry, after
  * the x prologue, first row group landed, end of the walk.  kernel 1: the
- * batched MFMA walk at B <= 32, 65 per wave at (workgroup * 8 + wave) * 65:
+ * batched MFMA walk at B <= 32, 68 per wave at (workgroup * 8 + wave) * 68:
  * entry, then per super-block step (up to 16) after the barrier, weights
- * parked, next x staged, MFMAs folded.  No counterpart in the reference; a
+ * parked, next x staged, MFMAs folded; then the split-K epilogue's partials
+ * acknowledged, arrival counted, end of the last split's sums and stores.  No counterpart in the reference; a
  * profiling aid. */
 int jh_debug_timeline(int device, int kernel, uint64_t *out, size_t n);
 

@@ -53,9 +53,11 @@ constexpr int kMinWorkgroups = 256;  // split K until the grid has this many
 // Timeline builds (-DJH_TIMELINE, juno_amd/timeline.py; never the shipped
 // library): per wave of the B <= 32 double-buffered walk, s_memrealtime at entry
 // and, per super-block step, after the step's barrier, once its weight chunks
-// are parked, once the next x is staged, and after its MFMAs and fold.
+// are parked, once the next x is staged, and after its MFMAs and fold; then in
+// the epilogue (store_tile) once its partials are acknowledged, once the
+// arrival is counted, and at its end.
 #ifdef JH_TIMELINE
-constexpr int kMtWg = 512, kMtSteps = 16, kMtPer = 1 + 4 * kMtSteps;
+constexpr int kMtWg = 512, kMtSteps = 16, kMtEpi = 1 + 4 * kMtSteps, kMtPer = kMtEpi + 3;
 __device__ unsigned long long g_mtimeline[kMtWg * 8 * kMtPer];
 #define JH_MT(slot)                                                                                         \
     do {                                                                                                    \
@@ -678,6 +680,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&tot)[NT], int r, int n
     // (buffer_wbl2), which measured ~100 us per GEMV; there are no non-atomic
     // stores for it to publish.
     __builtin_amdgcn_s_waitcnt(0);  // this wave's partials have reached the coherence point
+    JH_MT(kMtEpi);
     __shared__ int s_last;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -687,6 +690,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&tot)[NT], int r, int n
         s_last = last;
     }
     __syncthreads();
+    JH_MT(kMtEpi + 1);
     if (!s_last || !live) return;
     // KB splits' partials in flight at a time, added in split order
     constexpr int KB = 4 / NT;
@@ -727,6 +731,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&tot)[NT], int r, int n
             const int b = batch_of(n, i, kh);
             if (b < B) Y[(size_t)b * nrows + r] = acc[n][i];
         }
+    JH_MT(kMtEpi + 2);
 }
 
 // ------------------------------------------------------------------ batched kernel

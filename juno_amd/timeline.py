@@ -146,7 +146,7 @@ def run_child_mfma(B: int = 32) -> dict:
     hs0 = (V * 2)(mats[0][0].handle, mats[0][1].handle)
     if L.jh_qmatvec_batched_plan(2, hs0, B, ctypes.byref(kernel), ctypes.byref(ksplit)):
         raise RuntimeError(_lib.last_error())
-    per = 65
+    per = 68  # entry, 4 per step (16 steps), 3 in the epilogue
     n_slots = 512 * 8 * per
     buf = (ctypes.c_uint64 * n_slots)()
     launches = []
@@ -168,8 +168,9 @@ def run_child_mfma(B: int = 32) -> dict:
                 continue
             t = np.frombuffer(buf, dtype=np.uint64).reshape(-1, per).astype(np.int64)
             t = t[t[:, 0] > 0]
-            steps = int(((t[:, 1:] > 0).sum(axis=1) // 4).min())
+            steps = int(((t[:, 1:65] > 0).sum(axis=1) // 4).min())
             base = t[:, 0].min()
+            epi = (t[:, 65:68] - base) * TICK_NS / 1e3  # partials acknowledged, arrival counted, end (last split)
             rel = (t[:, : 1 + 4 * steps] - base) * TICK_NS / 1e3
             st = rel[:, 1:].reshape(len(rel), steps, 4)
             prev = np.concatenate([rel[:, :1], st[:, :-1, 3]], axis=1)  # end of the previous step
@@ -178,7 +179,13 @@ def run_child_mfma(B: int = 32) -> dict:
             d = {"waves": int(len(rel)), "steps": steps, "event_us": float(e0.elapsed_time(e1) * 1e3),
                  "start_p50": _pct(rel[:, 0], 50), "start_max": float(rel[:, 0].max()),
                  "first_step_p50": _pct(st[:, 0, 0], 50), "walk_end_p50": _pct(st[:, -1, 3], 50),
-                 "walk_end_max": float(st[:, -1, 3].max())}
+                 "walk_end_max": float(st[:, -1, 3].max()),
+                 "acked_p50": _pct(epi[:, 0] - st[:, -1, 3], 50), "acked_p90": _pct(epi[:, 0] - st[:, -1, 3], 90),
+                 "counted_p50": _pct(epi[:, 1] - epi[:, 0], 50), "counted_p90": _pct(epi[:, 1] - epi[:, 0], 90)}
+            last = t[:, 67] > 0  # waves of the splits that summed the partials
+            if last.any():
+                d["sum_store_p50"] = _pct(epi[last, 2] - epi[last, 1], 50)
+                d["end_max"] = float(epi[last, 2].max())
             for k, v in parts.items():
                 d[k + "_first"] = _pct(v[:, 0], 50)
                 d[k + "_rest"] = _pct(v[:, 1:], 50) if steps > 1 else 0.0
@@ -195,7 +202,7 @@ def summary_mfma(res: dict) -> str:
     ls = res["launches"]
 
     def med(k):
-        return float(np.median([d[k] for d in ls]))
+        return float(np.median([d.get(k, float("nan")) for d in ls]))
     out = [f"B = {res['B']}, plan kernel {res['kernel']} K split {res['ksplit']}, {ls[0]['waves']} waves, "
            f"{ls[0]['steps']} super-block steps per wave; medians over {len(ls)} launches.", "",
            "| quantity (µs) | value |", "|---|---:|",
@@ -203,6 +210,10 @@ def summary_mfma(res: dict) -> str:
            f"| waves started: median / last | {med('start_p50'):.2f} / {med('start_max'):.2f} |",
            f"| first step's barrier passed (median wave) | {med('first_step_p50'):.2f} |",
            f"| walk end: median wave / last wave | {med('walk_end_p50'):.2f} / {med('walk_end_max'):.2f} |",
+           f"| epilogue: partials acknowledged after the walk, median (p90) | {med('acked_p50'):.2f} ({med('acked_p90'):.2f}) |",
+           f"| epilogue: arrival counted after that, median (p90) | {med('counted_p50'):.2f} ({med('counted_p90'):.2f}) |",
+           f"| epilogue (last split): partial sums and stores, median | {med('sum_store_p50'):.2f} |",
+           f"| last wave done | {med('end_max'):.2f} |",
            "", "| per step, median wave (p90) | first step | later steps |", "|---|---:|---:|"]
     for k in ("barrier", "park", "stage_issue", "mfma_fold"):
         out.append(f"| {k} | {med(k + '_first'):.2f} | {med(k + '_rest'):.2f} ({med(k + '_rest_p90'):.2f}) |")
