@@ -628,6 +628,14 @@ __global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ 
     out += (size_t)z * gridDim.x * head_dim;
     const int T = min(*d_pos, max_seq - 1) + 1, nch = min((T + tc - 1) / tc, 1024);
     const float *ph = part + (size_t)h * nchmax * (head_dim + 2);
+    // the first kPre chunks' o of this thread's first dimension, loaded now: they
+    // do not depend on the weights, so their round trip overlaps the one of the
+    // maxima instead of following it
+    constexpr int kPre = 16;
+    float opre[kPre];
+#pragma unroll
+    for (int u = 0; u < kPre; u++)
+        opre[u] = (tid < head_dim && u < nch) ? ph[u * (head_dim + 2) + 2 + tid] : 0.f;
     float M = -INFINITY;
     for (int c = tid; c < nch; c += 256) {
         const float m = ph[c * (head_dim + 2)];
@@ -653,6 +661,12 @@ __global__ __launch_bounds__(256) void attn_combine_k(const float *__restrict__ 
         const float *op = ph + 2 + d;
         float o = 0.f;
         int c = 0;
+        if (d == tid) {  // the prefetched chunks, in chunk order
+#pragma unroll
+            for (int u = 0; u < kPre; u++)
+                if (u < nch) o = fmaf(opre[u], wc[u], o);
+            c = min(nch, kPre);
+        }
         for (; c + 8 <= nch; c += 8) {
             float v[8];
 #pragma unroll
