@@ -1103,6 +1103,11 @@ int jh_rope_attention_qmatvec_dev(const float *q, const float *k, const float *v
     if ((long long)wo->cols != (long long)n_heads * head_dim)
         return fail(JH_EINVAL, "wo has %d columns, attention gives n_heads * head_dim = %lld", wo->cols,
                     (long long)n_heads * head_dim);
+    {  // y is written while att is read (and, fused, while att is written)
+        const uintptr_t a0 = reinterpret_cast<uintptr_t>(d_att), a1 = a0 + sizeof(float) * (size_t)wo->cols;
+        const uintptr_t y0 = reinterpret_cast<uintptr_t>(d_y), y1 = y0 + sizeof(float) * (size_t)wo->rows;
+        if (a0 < y1 && y0 < a1) return fail(JH_EINVAL, "att and y must not overlap");
+    }
     int dev = 0;
     JH_HIP("hipGetDevice", hipGetDevice(&dev));
     void *ws = nullptr;

@@ -134,6 +134,11 @@ def test_attention_output_projection_arguments():
         rc = L.jh_rope_attention_qmatvec_dev(P(d), P(d), P(d), 16, 8, 64, P(pos), 4, ctypes.c_float(1e4), P(d), P(d),
                                              m.handle, None, P(d), None)
         assert rc == _lib.JH_EINVAL
+        # att and y overlap
+        y = torch.zeros(4096, device="cuda")
+        rc = L.jh_rope_attention_qmatvec_dev(P(d), P(d), P(d), 16, 8, 64, P(pos), 4, ctypes.c_float(1e4), P(d), P(d),
+                                             m.handle, P(y), V(y.data_ptr() + 4 * 100), None)
+        assert rc == _lib.JH_EINVAL and "overlap" in _lib.last_error()
     finally:
         m.close()
 
