@@ -220,15 +220,16 @@ constexpr int kRing = 4;  // cells per slot of the column-tile ring (a power of 
 __device__ unsigned int g_sync_faults;
 
 // Timeline builds (-DJH_TIMELINE, juno_amd/timeline.py; never the shipped
-// library): per wave of the DYN walk, s_memrealtime (100 MHz) at entry, after
-// the x prologue's barrier, once the first row group has landed, and at the end
-// of the walk; slot = (workgroup * 16 + wave) * 4, the last launch's values.
+// library): per wave of a shared-image walk (DYN, or column tiles), s_memrealtime
+// (100 MHz) at entry, after the x prologue's barrier, once the first row group
+// has landed, and at the end of the walk; slot = (workgroup * NW + wave) * 4,
+// the last launch's values.
 #ifdef JH_TIMELINE
 constexpr int kTlWaves = 4096;
 __device__ unsigned long long g_timeline[kTlWaves * 4];
 #define JH_TL(k)                                                                                       \
     do {                                                                                               \
-        if (DYN && (threadIdx.x & 63) == 0 && (int)blockIdx.x * NW + wave < kTlWaves)                  \
+        if (SX && (threadIdx.x & 63) == 0 && (int)blockIdx.x * NW + wave < kTlWaves)                   \
             g_timeline[((int)blockIdx.x * NW + wave) * 4 + (k)] = __builtin_amdgcn_s_memrealtime();    \
     } while (0)
 #else
@@ -1013,7 +1014,10 @@ __device__ __forceinline__ void gemv_staged_body(const StagedArgs &args) {
                     __hip_atomic_store(ring_done + cell, use + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
             }
-            if (next >= ngroups) break;
+            if (next >= ngroups) {
+                JH_TL(3);
+                break;
+            }
         } else {
             float *pp = part + (it & 1) * NW * R;
             if (lane == 63)

@@ -6,6 +6,7 @@ GPU box:
 
     python -m juno_amd.timeline build    # juno_amd/_timeline/libjunohip.so, compiled with -DJH_TIMELINE
     python -m juno_amd.timeline run      # the launches and the summary (markdown on stdout)
+    python -m juno_amd.timeline down     # the same for the Q6_K ffn_down (column-tiled rows)
     python -m juno_amd.timeline mfma 32  # the batched MFMA walk at B <= 32 (per super-block step)
 
 The instrumented build stamps s_memrealtime (100 MHz) per wave of the DYN walk
@@ -46,7 +47,9 @@ def _pct(a, q):
     return float(np.percentile(a, q))
 
 
-def run_child() -> dict:
+def run_child(kind: str = "gate_up") -> dict:
+    """kind gate_up: the grouped Q4_K [gate, up] launch; down: the Q6_K ffn_down
+    (4096 x 14336, column-tiled rows)."""
     import ctypes
 
     import numpy as np
@@ -60,17 +63,19 @@ def run_child() -> dict:
     s = torch.cuda.current_stream()
     g = torch.Generator(device="cuda")
     g.manual_seed(3)
+    down = kind == "down"
+    n, qt, rows, cols = (1, mv.Q6_K, HIDDEN, FFN) if down else (2, mv.Q4_K, FFN, HIDDEN)
     mats = []
     for _ in range(LAYERS):
         pair = []
-        for _ in range(2):
-            w = torch.randn(FFN * HIDDEN, generator=g, device="cuda").mul_(0.02)
-            pair.append(be.quantize_dev(mv.Q4_K, w.data_ptr(), FFN, HIDDEN, s.cuda_stream))
+        for _ in range(n):
+            w = torch.randn(rows * cols, generator=g, device="cuda").mul_(0.02)
+            pair.append(be.quantize_dev(qt, w.data_ptr(), rows, cols, s.cuda_stream))
             del w
         mats.append(pair)
     torch.cuda.synchronize()
-    x = torch.randn(HIDDEN, generator=g, device="cuda")
-    ys = [torch.empty(FFN, device="cuda") for _ in range(2)]
+    x = torch.randn(cols, generator=g, device="cuda")
+    ys = [torch.empty(rows, device="cuda") for _ in range(n)]
     V = ctypes.c_void_p
     n_slots = 4096 * 4
     buf = (ctypes.c_uint64 * n_slots)()
@@ -78,12 +83,12 @@ def run_child() -> dict:
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for rep in range(REPS + 1):
         for pair in mats:
-            hs = (V * 2)(pair[0].handle, pair[1].handle)
-            xs = (V * 2)(x.data_ptr(), x.data_ptr())
-            yp = (V * 2)(ys[0].data_ptr(), ys[1].data_ptr())
+            hs = (V * n)(*[m.handle for m in pair])
+            xs = (V * n)(*[x.data_ptr()] * n)
+            yp = (V * n)(*[y.data_ptr() for y in ys])
             ctypes.memset(buf, 0, ctypes.sizeof(buf))
             e0.record(s)
-            if L.jh_qmatvec_group_dev(2, hs, xs, yp, V(s.cuda_stream)):
+            if L.jh_qmatvec_group_dev(n, hs, xs, yp, V(s.cuda_stream)):
                 raise RuntimeError(_lib.last_error())
             e1.record(s)
             torch.cuda.synchronize()
@@ -109,7 +114,8 @@ def run_child() -> dict:
     for pair in mats:
         for m in pair:
             m.close()
-    return {"launches": launches}
+    return {"launches": launches, "kind": kind,
+            "bytes": n * rows * (cols // 256) * (210 if down else 144) + 4 * (cols + n * rows)}
 
 
 def run_child_mfma(B: int = 32) -> dict:
@@ -223,7 +229,7 @@ def summary_mfma(res: dict) -> str:
 def summary(res: dict) -> str:
     import numpy as np
     ls = res["launches"]
-    bytes_launch = 2 * FFN * (HIDDEN // 256) * 144 + 4 * (HIDDEN + 2 * FFN)
+    bytes_launch = res.get("bytes", 2 * FFN * (HIDDEN // 256) * 144 + 4 * (HIDDEN + 2 * FFN))
 
     def med(k):
         return float(np.median([d[k] for d in ls]))
@@ -254,7 +260,7 @@ def main(argv) -> None:
         print(build())
         return
     if cmd == "child":
-        print(json.dumps(run_child()))
+        print(json.dumps(run_child(argv[2] if len(argv) > 2 else "gate_up")))
         return
     if cmd == "child_mfma":
         print(json.dumps(run_child_mfma(int(argv[2]) if len(argv) > 2 else 32)))
@@ -263,14 +269,14 @@ def main(argv) -> None:
         raise SystemExit(f"{LIB} is not built: run `python -m juno_amd.timeline build` first")
     env = dict(os.environ, JUNO_LIB_PATH=LIB, JH_EXTRA_FLAGS=FLAGS)
     mfma = cmd == "mfma"
-    child = ["child_mfma", argv[2] if len(argv) > 2 else "32"] if mfma else ["child"]
+    child = ["child_mfma", argv[2] if len(argv) > 2 else "32"] if mfma else ["child", "down" if cmd == "down" else "gate_up"]
     r = subprocess.run([sys.executable, "-m", "juno_amd.timeline", *child], env=env, capture_output=True, text=True,
                        cwd=os.path.dirname(HERE))
     if r.returncode:
         raise SystemExit(r.stderr[-4000:])
     res = json.loads(r.stdout.strip().splitlines()[-1])
     print(summary_mfma(res) if mfma else summary(res))
-    # run [json], mfma [B [json]]
+    # run [json], down [json], mfma [B [json]]
     out = (argv[3] if len(argv) > 3 else None) if mfma else (argv[2] if len(argv) > 2 else None)
     if out:
         with open(out, "w") as f:
