@@ -47,6 +47,67 @@ def _pct(a, q):
     return float(np.percentile(a, q))
 
 
+def staged_launch_stats(raw, waves_per_wg: int = 16) -> dict:
+    """One launch's staged-walk stamps (4 per wave: entry, prologue barrier,
+    first row group landed, walk end; 0 for waves that did not run), in µs
+    from the launch's earliest wave start."""
+    import numpy as np
+    t = np.asarray(raw, dtype=np.uint64).reshape(-1, 4).astype(np.int64)
+    t = t[t[:, 0] > 0]
+    base = t[:, 0].min()
+    rel = (t - base) * TICK_NS / 1e3
+    wg_end = rel[:, 3].reshape(-1, waves_per_wg).max(axis=1)
+    return {
+        "waves": int(len(rel)),
+        "start_p50": _pct(rel[:, 0], 50), "start_p90": _pct(rel[:, 0], 90), "start_max": float(rel[:, 0].max()),
+        "prologue_p50": _pct(rel[:, 1], 50), "prologue_p90": _pct(rel[:, 1], 90),
+        "first_rows_p10": _pct(rel[:, 2], 10), "first_rows_p50": _pct(rel[:, 2], 50),
+        "first_rows_p90": _pct(rel[:, 2], 90),
+        "wg_end_min": float(wg_end.min()), "wg_end_p10": _pct(wg_end, 10), "wg_end_p50": _pct(wg_end, 50),
+        "wg_end_p90": _pct(wg_end, 90), "end": float(rel[:, 3].max()),
+    }
+
+
+MFMA_PER_WAVE = 68  # entry, 4 per super-block step (up to 16), 3 in the split-K epilogue
+
+
+def mfma_launch_stats(raw) -> dict:
+    """One launch's batched-walk stamps (MFMA_PER_WAVE per wave), in µs from the
+    launch's earliest wave start: per step, the wait at its barrier (from the
+    previous step's fold, or from entry for the first), the park, the staging
+    of the next x and the MFMAs and fold; then the epilogue."""
+    import numpy as np
+    t = np.asarray(raw, dtype=np.uint64).reshape(-1, MFMA_PER_WAVE).astype(np.int64)
+    t = t[t[:, 0] > 0]
+    steps = int(((t[:, 1:65] > 0).sum(axis=1) // 4).min())
+    base = t[:, 0].min()
+    epi = (t[:, 65:68] - base) * TICK_NS / 1e3  # partials acknowledged, arrival counted, end (last split)
+    rel = (t[:, : 1 + 4 * steps] - base) * TICK_NS / 1e3
+    st = rel[:, 1:].reshape(len(rel), steps, 4)
+    prev = np.concatenate([rel[:, :1], st[:, :-1, 3]], axis=1)  # end of the previous step
+    parts = {"barrier": st[:, :, 0] - prev, "park": st[:, :, 1] - st[:, :, 0],
+             "stage_issue": st[:, :, 2] - st[:, :, 1], "mfma_fold": st[:, :, 3] - st[:, :, 2]}
+    d = {"waves": int(len(rel)), "steps": steps,
+         "start_p50": _pct(rel[:, 0], 50), "start_max": float(rel[:, 0].max()),
+         "first_step_p50": _pct(st[:, 0, 0], 50), "walk_end_p50": _pct(st[:, -1, 3], 50),
+         "walk_end_max": float(st[:, -1, 3].max())}
+    acked = t[:, 65] > 0  # waves that went through the split-K hand-off
+    if acked.any():
+        d["acked_p50"] = _pct(epi[acked, 0] - st[acked, -1, 3], 50)
+        d["acked_p90"] = _pct(epi[acked, 0] - st[acked, -1, 3], 90)
+        d["counted_p50"] = _pct(epi[acked, 1] - epi[acked, 0], 50)
+        d["counted_p90"] = _pct(epi[acked, 1] - epi[acked, 0], 90)
+    last = t[:, 67] > 0  # waves of the splits that summed the partials
+    if last.any():
+        d["sum_store_p50"] = _pct(epi[last, 2] - epi[last, 1], 50)
+        d["end_max"] = float(epi[last, 2].max())
+    for k, v in parts.items():
+        d[k + "_first"] = _pct(v[:, 0], 50)
+        d[k + "_rest"] = _pct(v[:, 1:], 50) if steps > 1 else 0.0
+        d[k + "_rest_p90"] = _pct(v[:, 1:], 90) if steps > 1 else 0.0
+    return d
+
+
 def run_child(kind: str = "gate_up") -> dict:
     """kind gate_up: the grouped Q4_K [gate, up] launch; down: the Q6_K ffn_down
     (4096 x 14336, column-tiled rows)."""
@@ -96,21 +157,9 @@ def run_child(kind: str = "gate_up") -> dict:
                 raise RuntimeError(_lib.last_error())
             if rep == 0:
                 continue  # warm-up pass
-            t = np.frombuffer(buf, dtype=np.uint64).reshape(-1, 4).astype(np.int64)
-            t = t[t[:, 0] > 0]
-            base = t[:, 0].min()
-            rel = (t - base) * TICK_NS / 1e3  # us
-            wg_end = rel[:, 3].reshape(-1, 16).max(axis=1)
-            launches.append({
-                "waves": int(len(rel)),
-                "event_us": float(e0.elapsed_time(e1) * 1e3),
-                "start_p50": _pct(rel[:, 0], 50), "start_p90": _pct(rel[:, 0], 90), "start_max": float(rel[:, 0].max()),
-                "prologue_p50": _pct(rel[:, 1], 50), "prologue_p90": _pct(rel[:, 1], 90),
-                "first_rows_p10": _pct(rel[:, 2], 10), "first_rows_p50": _pct(rel[:, 2], 50),
-                "first_rows_p90": _pct(rel[:, 2], 90),
-                "wg_end_min": float(wg_end.min()), "wg_end_p10": _pct(wg_end, 10), "wg_end_p50": _pct(wg_end, 50),
-                "wg_end_p90": _pct(wg_end, 90), "end": float(rel[:, 3].max()),
-            })
+            d = staged_launch_stats(np.frombuffer(buf, dtype=np.uint64))
+            d["event_us"] = float(e0.elapsed_time(e1) * 1e3)
+            launches.append(d)
     for pair in mats:
         for m in pair:
             m.close()
@@ -152,8 +201,7 @@ def run_child_mfma(B: int = 32) -> dict:
     hs0 = (V * 2)(mats[0][0].handle, mats[0][1].handle)
     if L.jh_qmatvec_batched_plan(2, hs0, B, ctypes.byref(kernel), ctypes.byref(ksplit)):
         raise RuntimeError(_lib.last_error())
-    per = 68  # entry, 4 per step (16 steps), 3 in the epilogue
-    n_slots = 512 * 8 * per
+    n_slots = 512 * 8 * MFMA_PER_WAVE
     buf = (ctypes.c_uint64 * n_slots)()
     launches = []
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -172,30 +220,8 @@ def run_child_mfma(B: int = 32) -> dict:
                 raise RuntimeError(_lib.last_error())
             if rep == 0:
                 continue
-            t = np.frombuffer(buf, dtype=np.uint64).reshape(-1, per).astype(np.int64)
-            t = t[t[:, 0] > 0]
-            steps = int(((t[:, 1:65] > 0).sum(axis=1) // 4).min())
-            base = t[:, 0].min()
-            epi = (t[:, 65:68] - base) * TICK_NS / 1e3  # partials acknowledged, arrival counted, end (last split)
-            rel = (t[:, : 1 + 4 * steps] - base) * TICK_NS / 1e3
-            st = rel[:, 1:].reshape(len(rel), steps, 4)
-            prev = np.concatenate([rel[:, :1], st[:, :-1, 3]], axis=1)  # end of the previous step
-            parts = {"barrier": st[:, :, 0] - prev, "park": st[:, :, 1] - st[:, :, 0],
-                     "stage_issue": st[:, :, 2] - st[:, :, 1], "mfma_fold": st[:, :, 3] - st[:, :, 2]}
-            d = {"waves": int(len(rel)), "steps": steps, "event_us": float(e0.elapsed_time(e1) * 1e3),
-                 "start_p50": _pct(rel[:, 0], 50), "start_max": float(rel[:, 0].max()),
-                 "first_step_p50": _pct(st[:, 0, 0], 50), "walk_end_p50": _pct(st[:, -1, 3], 50),
-                 "walk_end_max": float(st[:, -1, 3].max()),
-                 "acked_p50": _pct(epi[:, 0] - st[:, -1, 3], 50), "acked_p90": _pct(epi[:, 0] - st[:, -1, 3], 90),
-                 "counted_p50": _pct(epi[:, 1] - epi[:, 0], 50), "counted_p90": _pct(epi[:, 1] - epi[:, 0], 90)}
-            last = t[:, 67] > 0  # waves of the splits that summed the partials
-            if last.any():
-                d["sum_store_p50"] = _pct(epi[last, 2] - epi[last, 1], 50)
-                d["end_max"] = float(epi[last, 2].max())
-            for k, v in parts.items():
-                d[k + "_first"] = _pct(v[:, 0], 50)
-                d[k + "_rest"] = _pct(v[:, 1:], 50) if steps > 1 else 0.0
-                d[k + "_rest_p90"] = _pct(v[:, 1:], 90) if steps > 1 else 0.0
+            d = mfma_launch_stats(np.frombuffer(buf, dtype=np.uint64))
+            d["event_us"] = float(e0.elapsed_time(e1) * 1e3)
             launches.append(d)
     for pair in mats:
         for m in pair:
