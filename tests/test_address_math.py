@@ -14,9 +14,9 @@ The MFMA model's plan (K split, prepared x or not) is checked against the
 library's planner (jh_qmatvec_batched_plan), so the model walks the same
 launches the library makes.
 
-This is the check that round 1's unexplained hipErrorIllegalAddress (the first
-eager B = 32 MFMA launch of a bench run) called for: it finds every access of
-the current kernels in bounds at every configuration the BASELINE names.
+It was written for an unexplained hipErrorIllegalAddress seen once on the
+first eager B = 32 MFMA launch of a bench run: it finds every access of the
+current kernels in bounds at every benchmark configuration.
 """
 import ctypes
 
